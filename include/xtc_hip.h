@@ -1,0 +1,204 @@
+/*
+ * SPDX-License-Identifier: BSD-3-Clause
+ *
+ * xtc_hip.h -- C-ABI of libxtc_hip.so, the MI355X (gfx950) execution backend
+ * of XTC.  Plain pointers and sizes only; every entry point returns 0 on
+ * success and a non-zero status otherwise, with the message available from
+ * xtc_hip_last_error().
+ *
+ * The library has three groups of entry points:
+ *
+ *  1. Device runtime.  Replaces the mgpu* calls that the reference's
+ *     GPUDevice binds through ctypes
+ *     (src/xtc/runtimes/accelerator/gpu/GPUDevice.py:36-63,131-207:
+ *     mgpuStreamCreate, mgpuMemAlloc, mgpuMemFree, mgpuMemcpy,
+ *     mgpuStreamSynchronize).  Host buffers are never registered for
+ *     zero-copy access (GPUDevice.py:327-347 mgpuMemHostRegister): tensors are
+ *     copied to HBM explicitly, so kernels always read device memory.
+ *
+ *  2. Operator entry points.  A compiled XTC module is a shared object that
+ *     exports `void <graph.name>(void *in0, ..., void *out0, ...)`
+ *     (src/xtc/backends/mlir/MlirGraphBackend.py:125-171,
+ *     src/xtc/backends/mlir/MlirTarget/MlirLLVMTarget.py:311).  The HIP
+ *     compiler emits that function as a few calls to the entry points below,
+ *     one per scheduled graph node, followed by xtc_hip_synchronize(), since
+ *     callers time the payload with a wall clock around the call
+ *     (src/xtc/csrcs/runtimes/host/evaluate_perf.c:92-120).  All operands are
+ *     device pointers to dense row-major (C-contiguous) buffers.
+ *
+ *  3. Timing harness.  Same protocol and signature as the reference runtime's
+ *     evaluate_perf / evaluate (src/xtc/csrcs/runtimes/host/evaluate_perf.c:
+ *     187-248, bound in src/xtc/runtimes/host/runtime.py:41-145) and the
+ *     peak estimate evaluate_flops (evaluate_flops.c:461-494).
+ */
+#ifndef XTC_HIP_H
+#define XTC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *xtc_hip_last_error(void);
+
+/* ---------------------------------------------------------- device runtime */
+
+/* Number of visible GPUs (0 when no GPU/driver); never initialises a device. */
+int xtc_hip_device_count(void);
+
+/* Selects `device` on the calling thread and creates the library stream
+ * (default priority).  Idempotent.  Replaces GPUDevice.__init_once__
+ * (GPUDevice.py:45-63). */
+int xtc_hip_init(int device);
+
+/* gcnArchName ("gfx950:sramecc+:xnack-") and marketing name of the device. */
+int xtc_hip_device_arch(char *buf, int len);
+int xtc_hip_device_name(char *buf, int len);
+
+/* The library stream (hipStream_t) used when a descriptor's stream is NULL. */
+void *xtc_hip_stream(void);
+
+/* Waits for all work on the library stream (mgpuStreamSynchronize). */
+int xtc_hip_synchronize(void);
+
+/* Device memory (mgpuMemAlloc / mgpuMemFree). NULL on failure. */
+void *xtc_hip_malloc(uint64_t bytes);
+int xtc_hip_free(void *ptr);
+
+/* Synchronous copies on the library stream (mgpuMemcpy + sync). */
+int xtc_hip_memcpy_h2d(void *dst_device, const void *src_host, uint64_t bytes);
+int xtc_hip_memcpy_d2h(void *dst_host, const void *src_device, uint64_t bytes);
+int xtc_hip_memcpy_d2d(void *dst_device, const void *src_device, uint64_t bytes);
+
+/* Zero-fills device memory with a kernel (AcceleratorDevice.memory_fill_zero,
+ * src/xtc/itf/runtime/accelerator.py:104-112). */
+int xtc_hip_memset_zero(void *ptr, uint64_t bytes);
+
+/* Events on the library stream, for kernel-only timing. */
+void *xtc_hip_event_create(void);
+int xtc_hip_event_record(void *event, void *stream);
+int xtc_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+int xtc_hip_event_destroy(void *event);
+
+/* ------------------------------------------------------ operator entry points */
+
+enum xtc_hip_dtype { XTC_HIP_F32 = 0, XTC_HIP_BF16 = 1 };
+
+/* Kernel template parameters a schedule maps to (block tile BM x BN, K slab
+ * BK, WGM x WGN waves).  All zero means "library default for the shape". */
+typedef struct {
+  int bm, bn, bk, wgm, wgn;
+} xtc_hip_tile;
+
+/* C[M,N] = relu?( A[M,K] @ B[K,N] + bias[N]? ), fp32 output.
+ * Replaces the scheduled linalg.fill + linalg.matmul pair of
+ * MlirOperatorMatmul.generate_op (src/xtc/backends/mlir/MlirOps.py:189-270),
+ * with XTCOperMatmul semantics (src/xtc/graphs/xtc/operators.py:159-221):
+ * A is the input viewed as (shape[0], prod(rest)), B as (prod(rest[:-1]),
+ * last).  The relu node of XTCOperRelu (operators.py:224-249) may be fused
+ * as the epilogue: out = max(out, relu_threshold), NaN preserved. */
+typedef struct {
+  int dtype;             /* xtc_hip_dtype of A and B; C is always fp32 */
+  int M, N, K;
+  int lda, ldb, ldc;     /* row strides in elements, 0 = dense */
+  xtc_hip_tile tile;
+  int split_k;           /* >= 1: K partitions reduced by a second kernel */
+  int group_m;           /* raster group height in tiles, 0 = default */
+  int xcd_remap;         /* 1 = map consecutive tiles onto one XCD */
+  int relu;
+  float relu_threshold;
+  void *stream;          /* hipStream_t, NULL = library stream */
+} xtc_hip_matmul_desc;
+
+int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B,
+                   float *C, const float *bias);
+
+/* O[b,oh,ow,f] = relu?( sum_{r,s,c} Ipad[b,oh*sh+r,ow*sw+s,c] * W[r,s,c,f] )
+ * NHWC x RSCF -> NHWC (XTCOperConv2D, operators.py:252-347;
+ * MlirOperatorConv2D, MlirOps.py:304-441).  Ipad is I padded by
+ * (pad_top, pad_bottom, pad_left, pad_right) with pad_value: the XTCOperPad2D
+ * producer (operators.py:350-591, MlirOps.py:719-735) fused into the loader.
+ * C must be a multiple of 4 (fp32) or 8 (bf16). */
+typedef struct {
+  int dtype;
+  int N, H, W, C;        /* unpadded input */
+  int F, R, S;
+  int stride_h, stride_w;
+  int pad_top, pad_bottom, pad_left, pad_right;
+  float pad_value;
+  xtc_hip_tile tile;
+  int split_k;
+  int group_m;
+  int xcd_remap;
+  int relu;
+  float relu_threshold;
+  void *stream;
+} xtc_hip_conv2d_desc;
+
+int xtc_hip_conv2d(const xtc_hip_conv2d_desc *desc, const void *input,
+                   const void *weight, float *out, const float *bias);
+
+/* y[i] = max(x[i], threshold) over n fp32 elements (XTCOperRelu forward,
+ * operators.py:224-249); x == y allowed. */
+int xtc_hip_relu(const float *x, float *y, uint64_t n, float threshold,
+                 void *stream);
+
+/* Constant padding of a row-major fp32 tensor of rank <= 8: out has shape
+ * shape[d] + before[d] + after[d]; border = value, interior = input
+ * (_OperPadImpl.forward / np.pad, operators.py:413-433). */
+int xtc_hip_pad(const float *x, float *y, int ndim, const int64_t *shape,
+                const int64_t *before, const int64_t *after, float value,
+                void *stream);
+
+/* Round-to-nearest-even fp32 -> bf16 (stored as uint16) and back. */
+int xtc_hip_cast_f32_to_bf16(const float *x, uint16_t *y, uint64_t n, void *stream);
+int xtc_hip_cast_bf16_to_f32(const uint16_t *x, float *y, uint64_t n, void *stream);
+
+/* Compiled kernel instances.  A schedule maps onto one of these; the HIP
+ * Scheduler rejects schedules that map to none. */
+typedef struct {
+  int dtype;
+  int conv;              /* 1: implicit-GEMM conv loader */
+  xtc_hip_tile tile;
+  int lds_bytes;
+  int threads;
+} xtc_hip_gemm_instance;
+
+int xtc_hip_gemm_instance_count(void);
+int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance *out);
+
+/* Tile the library picks when a descriptor leaves `tile` zeroed. */
+int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile *out,
+                         int *split_k);
+
+/* ---------------------------------------------------------- timing harness */
+
+/* Same protocol as evaluate_perf (evaluate_perf.c:63-125): one warm-up call
+ * when number > 0, then for each of `repeat` repeats the call count doubles
+ * from `number` until a batch lasts >= min_repeat_ms; results[r] = batch
+ * seconds / calls.  With events: "gpu.time" gives device seconds per call
+ * measured by events bracketing the batch on the library stream;
+ * "gpu.clocks" the same in nanoseconds.  Unknown events yield -1.  func is
+ * called with nargs (<= 8) pointer arguments. */
+void xtc_hip_evaluate_perf(double *results, int events_num, const char *events_names[],
+                           int repeat, int number, int min_repeat_ms,
+                           void (*func)(void), void **args, int nargs);
+
+/* evaluate_perf without events (evaluate_perf.c:240-248). */
+void xtc_hip_evaluate(double *results, int repeat, int number, int min_repeat_ms,
+                      void (*func)(void), void **args, int nargs);
+
+/* Peak multiply-accumulates per second of the device for dtype ("float32",
+ * "bfloat16"): XTC counts one op per FMA (operation.py:76-82), so this is
+ * half the FLOP/s figure.  0.0 for unsupported dtypes. */
+double xtc_hip_evaluate_flops(const char *dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XTC_HIP_H */

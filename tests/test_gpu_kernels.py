@@ -1,0 +1,274 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""Parity of the HIP kernels (through the libxtc_hip C-ABI) against the oracle.
+
+Bars: bit-exact on integer known-answer inputs; otherwise
+max|out-ref| / (sqrt(K) max|A| max|B|) <= 1e-4 (fp32) or 1e-2 (bf16 inputs),
+with the oracle fed the same (bf16-rounded) values in float64.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import reference as ref
+from xtc_amd.runtimes.hip import capi
+from xtc_amd.runtimes.hip.buffer import DeviceBuffer, ensure_device
+from xtc_amd.utils.bf16 import f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ensure_device(0)
+    yield
+
+
+def _dev(a: np.ndarray, dtype: str) -> DeviceBuffer:
+    if dtype == "bfloat16":
+        return DeviceBuffer.from_numpy(f32_to_bf16_bits(a))
+    return DeviceBuffer.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+
+
+def run_matmul(a, b, dtype="float32", tile=None, split_k=0, relu=False, thr=0.0, bias=None):
+    M, K = a.shape
+    N = b.shape[1]
+    A, B = _dev(a, dtype), _dev(b, dtype)
+    C = DeviceBuffer(M * N * 4)
+    bias_buf = DeviceBuffer.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    d = capi.MatmulDesc()
+    d.dtype = capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16
+    d.M, d.N, d.K = M, N, K
+    if tile is not None:
+        d.tile = capi.Tile(*tile)
+    d.split_k = split_k
+    d.xcd_remap = 1
+    d.relu = int(relu)
+    d.relu_threshold = thr
+    L = capi.lib()
+    capi.check(
+        L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, bias_buf.c_ptr if bias_buf else None),
+        "matmul",
+    )
+    capi.check(L.xtc_hip_synchronize(), "sync")
+    return C.to_numpy((M, N), np.float32)
+
+
+def run_conv(x, w, dtype="float32", stride=(1, 1), pads=(0, 0, 0, 0), pad_value=0.0, tile=None, relu=False, split_k=0):
+    n, h, wd, c = x.shape
+    r, s, _, f = w.shape
+    I, W = _dev(x, dtype), _dev(w, dtype)
+    hp, wp = h + pads[0] + pads[1], wd + pads[2] + pads[3]
+    oh, ow = (hp - r) // stride[0] + 1, (wp - s) // stride[1] + 1
+    O = DeviceBuffer(n * oh * ow * f * 4)
+    d = capi.Conv2dDesc()
+    d.dtype = capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16
+    d.N, d.H, d.W, d.C, d.F, d.R, d.S = n, h, wd, c, f, r, s
+    d.stride_h, d.stride_w = stride
+    d.pad_top, d.pad_bottom, d.pad_left, d.pad_right = pads
+    d.pad_value = pad_value
+    if tile is not None:
+        d.tile = capi.Tile(*tile)
+    d.split_k = split_k
+    d.xcd_remap = 1
+    d.relu = int(relu)
+    L = capi.lib()
+    capi.check(L.xtc_hip_conv2d(ctypes.byref(d), I.c_ptr, W.c_ptr, O.c_ptr, None), "conv2d")
+    capi.check(L.xtc_hip_synchronize(), "sync")
+    return O.to_numpy((n, oh, ow, f), np.float32)
+
+
+def rng_uniform(seed, shape, low=-1.0, high=1.0):
+    return np.random.default_rng(seed).uniform(low, high, size=shape).astype(np.float32)
+
+
+# ------------------------------------------------------------------ matmul
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("shape", [(64, 64, 64), (512, 512, 512), (256, 128, 1024)])
+def test_matmul_integer_kat_exact(dtype, shape):
+    M, N, K = shape
+    a = ref.np_init((M, K), "float32")
+    b = ref.np_init((K, N), "float32")
+    out = run_matmul(a, b, dtype)
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
+
+
+def test_matmul_c1_seeded_fp32():
+    a, b = ref.config_inputs("C1")
+    out = run_matmul(a, b)
+    err = ref.scaled_error(out, ref.matmul(a, b), 512, 1.0, 1.0)
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize(
+    "shape", [(21, 32, 16), (100, 72, 40), (1, 8, 8), (257, 136, 64), (33, 264, 520), (5, 4, 3), (7, 6, 5)]
+)
+def test_matmul_ragged(dtype, shape):
+    M, N, K = shape
+    a = rng_uniform(1, (M, K))
+    b = rng_uniform(2, (K, N))
+    if dtype == "bfloat16":
+        a, b = ref.round_bf16(a), ref.round_bf16(b)
+    out = run_matmul(a, b, dtype)
+    err = ref.scaled_error(out, ref.matmul(a, b), K, np.abs(a).max(), np.abs(b).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+
+
+def _instances(conv: bool):
+    return [i for i in capi.gemm_instances() if i["conv"] == conv]
+
+
+def test_every_matmul_instance():
+    """Each compiled tile on a shape with partial tiles in M and N and K."""
+    failures = []
+    for inst in _instances(False):
+        bm, bn, bk, wgm, wgn = inst["tile"]
+        dtype = inst["dtype"]
+        vec = 4 if dtype == "float32" else 8
+        M, N, K = 2 * bm + 3, 2 * bn + vec, 3 * bk + vec
+        a = ref.np_init((M, K), "float32")
+        b = (ref.np_init((K, N), "float32")[::-1]).copy()
+        out = run_matmul(a, b, dtype, tile=inst["tile"])
+        expect = ref.matmul(a, b).astype(np.float32)
+        if not np.array_equal(out, expect):
+            failures.append((dtype, inst["tile"], float(np.abs(out - expect).max())))
+    assert not failures, failures[:10]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_matmul_split_k_bias_relu(dtype):
+    M, N, K = 96, 160, 2048
+    a = rng_uniform(3, (M, K))
+    b = rng_uniform(4, (K, N))
+    bias = rng_uniform(5, (N,))
+    if dtype == "bfloat16":
+        a, b = ref.round_bf16(a), ref.round_bf16(b)
+    out = run_matmul(a, b, dtype, split_k=8, relu=True, bias=bias)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    err = ref.scaled_error(out, expect, K, np.abs(a).max(), np.abs(b).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+    # relu applied after the full reduction
+    assert (out >= 0).all()
+
+
+def test_matmul_relu_threshold_nan():
+    a = np.ones((16, 8), np.float32)
+    b = np.ones((8, 16), np.float32)
+    a[0, 0] = np.nan
+    out = run_matmul(a, b, relu=True, thr=9.0)
+    assert np.isnan(out[0]).all()
+    np.testing.assert_array_equal(out[1:], np.full((15, 16), 9.0, np.float32))
+
+
+def test_matmul_c3b_skinny_bf16():
+    a, b = ref.config_inputs("C3b")
+    out = run_matmul(a, b, "bfloat16")
+    err = ref.scaled_error(out, ref.matmul(a, b), 8192, np.abs(a).max(), np.abs(b).max())
+    assert err <= TOL_BF16, err
+
+
+# ------------------------------------------------------------------ conv2d
+
+
+def test_conv_c4_pad_relu_fp32():
+    x, w = ref.config_inputs("C4")
+    out = run_conv(x, w, pads=(1, 1, 1, 1), relu=True)
+    xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    expect = ref.relu(ref.conv2d(xp, w))
+    err = ref.scaled_error(out, expect, 576, np.abs(xp).max(), np.abs(w).max())
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_conv_stride_asym_pad_value(dtype):
+    x = rng_uniform(6, (2, 9, 11, 16))
+    w = rng_uniform(7, (3, 2, 16, 24))
+    if dtype == "bfloat16":
+        x, w = ref.round_bf16(x), ref.round_bf16(w)
+    pads = (2, 1, 0, 3)
+    out = run_conv(x, w, dtype, stride=(2, 3), pads=pads, pad_value=0.5)
+    xp = ref.pad(x, [(0, 0), (2, 1), (0, 3), (0, 0)], 0.5)
+    expect = ref.conv2d(xp, w, (2, 3))
+    err = ref.scaled_error(out, expect, 3 * 2 * 16, 1.0, np.abs(w).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+
+
+def test_every_conv_instance():
+    failures = []
+    for inst in _instances(True):
+        dtype = inst["dtype"]
+        x = ref.np_init((2, 10, 12, 16), "float32")
+        w = (ref.np_init((3, 3, 16, 32), "float32")[::-1]).copy()
+        out = run_conv(x, w, dtype, pads=(1, 1, 1, 1), tile=inst["tile"])
+        xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+        expect = ref.conv2d(xp, w).astype(np.float32)
+        if not np.array_equal(out, expect):
+            failures.append((dtype, inst["tile"], float(np.abs(out - expect).max())))
+    assert not failures, failures[:10]
+
+
+def test_conv_unaligned_channels_fallback():
+    x = rng_uniform(8, (1, 7, 7, 3))
+    w = rng_uniform(9, (3, 3, 3, 5))
+    out = run_conv(x, w, pads=(1, 1, 1, 1))
+    expect = ref.conv2d(ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)]), w)
+    assert ref.scaled_error(out, expect, 27, 1.0, 1.0) <= TOL_F32
+
+
+# ------------------------------------------------------------- aux kernels
+
+
+def test_relu_kernel():
+    x = rng_uniform(10, (1000003,))
+    x[5] = np.nan
+    X = DeviceBuffer.from_numpy(x)
+    Y = DeviceBuffer(x.nbytes)
+    L = capi.lib()
+    capi.check(L.xtc_hip_relu(X.c_ptr, Y.c_ptr, x.size, ctypes.c_float(0.25), None))
+    capi.check(L.xtc_hip_synchronize())
+    y = Y.to_numpy(x.shape, np.float32)
+    np.testing.assert_array_equal(y, ref.relu(x, 0.25))
+
+
+def test_pad_kernel():
+    x = rng_uniform(11, (3, 5, 7, 4))
+    X = DeviceBuffer.from_numpy(x)
+    pads = [(0, 0), (1, 2), (3, 0), (0, 1)]
+    shape = (ctypes.c_int64 * 4)(*x.shape)
+    before = (ctypes.c_int64 * 4)(*[p[0] for p in pads])
+    after = (ctypes.c_int64 * 4)(*[p[1] for p in pads])
+    expect = ref.pad(x, pads, -2.0)
+    Y = DeviceBuffer(expect.nbytes)
+    L = capi.lib()
+    capi.check(L.xtc_hip_pad(X.c_ptr, Y.c_ptr, 4, shape, before, after, ctypes.c_float(-2.0), None))
+    capi.check(L.xtc_hip_synchronize())
+    np.testing.assert_array_equal(Y.to_numpy(expect.shape, np.float32), expect)
+
+
+def test_cast_bf16_roundtrip():
+    x = rng_uniform(12, (4099,), -100, 100)
+    x[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    X = DeviceBuffer.from_numpy(x)
+    H = DeviceBuffer(x.size * 2)
+    Y = DeviceBuffer(x.nbytes)
+    L = capi.lib()
+    capi.check(L.xtc_hip_cast_f32_to_bf16(X.c_ptr, H.c_ptr, x.size, None))
+    capi.check(L.xtc_hip_cast_bf16_to_f32(H.c_ptr, Y.c_ptr, x.size, None))
+    capi.check(L.xtc_hip_synchronize())
+    np.testing.assert_array_equal(H.to_numpy(x.shape, np.uint16), f32_to_bf16_bits(x))
+    np.testing.assert_array_equal(Y.to_numpy(x.shape, np.float32), ref.round_bf16(x))
+
+
+def test_memset_zero():
+    B = DeviceBuffer.from_numpy(np.ones(1031, np.uint8))
+    B.zero()
+    assert not B.to_numpy((1031,), np.uint8).any()

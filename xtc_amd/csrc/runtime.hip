@@ -1,0 +1,792 @@
+// SPDX-License-Identifier: BSD-3-Clause
+// libxtc_hip runtime: device management, operator dispatch, auxiliary
+// HBM-bound kernels and the timing harness behind include/xtc_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+
+#include <mutex>
+#include <string>
+
+#include "registry.hpp"
+#include "xtc_hip.h"
+
+using namespace xtc_hip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return 1;
+}
+
+#define HIP_TRY(expr)                                                          \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess)                                                      \
+      return fail("%s failed: %s", #expr, hipGetErrorString(e_));              \
+  } while (0)
+
+constexpr int kMaxDevices = 16;
+
+struct DeviceState {
+  bool ready = false;
+  hipStream_t stream = nullptr;
+  void* workspace = nullptr;   // split-K partial sums
+  size_t workspace_bytes = 0;
+  std::string arch, name;
+};
+
+std::mutex g_mutex;
+DeviceState g_dev[kMaxDevices];
+int g_current = -1;
+
+DeviceState* current_state() {
+  if (g_current < 0) return nullptr;
+  DeviceState* d = &g_dev[g_current];
+  return d->ready ? d : nullptr;
+}
+
+hipStream_t pick_stream(void* s) {
+  if (s) return (hipStream_t)s;
+  DeviceState* d = current_state();
+  return d ? d->stream : nullptr;
+}
+
+double now_s() {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+// Grows the per-device split-K workspace.  Returns null on failure.
+void* workspace(size_t bytes) {
+  DeviceState* d = current_state();
+  if (!d) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mutex);
+  if (d->workspace_bytes < bytes) {
+    if (d->workspace) {
+      hipStreamSynchronize(d->stream);
+      hipFree(d->workspace);
+      d->workspace = nullptr;
+      d->workspace_bytes = 0;
+    }
+    if (hipMalloc(&d->workspace, bytes) != hipSuccess) return nullptr;
+    d->workspace_bytes = bytes;
+  }
+  return d->workspace;
+}
+
+// ------------------------------------------------------------ aux kernels
+
+__global__ void fill_zero_kernel(uint4* p, uint64_t n16, unsigned char* tail, int ntail) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < n16; i += stride) p[i] = make_uint4(0, 0, 0, 0);
+  if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
+__global__ void relu_kernel(const float* __restrict__ x, float* __restrict__ y, uint64_t n,
+                            float thr) {
+  uint64_t n4 = n / 4;
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* y4 = reinterpret_cast<float4*>(y);
+  for (uint64_t j = i; j < n4; j += stride) {
+    float4 v = x4[j];
+    v.x = v.x < thr ? thr : v.x;
+    v.y = v.y < thr ? thr : v.y;
+    v.z = v.z < thr ? thr : v.z;
+    v.w = v.w < thr ? thr : v.w;
+    y4[j] = v;
+  }
+  for (uint64_t j = n4 * 4 + i; j < n; j += stride) {
+    float v = x[j];
+    y[j] = v < thr ? thr : v;
+  }
+}
+
+struct PadDims {
+  int ndim;
+  int64_t in_shape[8];
+  int64_t out_shape[8];
+  int64_t before[8];
+};
+
+__global__ void pad_kernel(const float* __restrict__ x, float* __restrict__ y, PadDims d,
+                           uint64_t total, float value) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < total; i += stride) {
+    uint64_t rem = i;
+    int64_t src = 0;
+    int64_t src_stride = 1;
+    bool inside = true;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      int64_t o = (int64_t)(rem % (uint64_t)d.out_shape[k]);
+      rem /= (uint64_t)d.out_shape[k];
+      int64_t s = o - d.before[k];
+      inside = inside && s >= 0 && s < d.in_shape[k];
+      src += s * src_stride;
+      src_stride *= d.in_shape[k];
+    }
+    float v = value;
+    if (inside) v = x[src];
+    y[i] = v;
+  }
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  unsigned u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+  unsigned r = ((u >> 16) & 1u) + 0x7fffu;
+  return (uint16_t)((u + r) >> 16);
+}
+
+__global__ void cast_f32_bf16_kernel(const float* x, uint16_t* y, uint64_t n) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) y[i] = f32_to_bf16_rne(x[i]);
+}
+
+__global__ void cast_bf16_f32_kernel(const uint16_t* x, float* y, uint64_t n) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) y[i] = __uint_as_float(((unsigned)x[i]) << 16);
+}
+
+// out[m][n] = epilogue( sum_s partial[s][m][n] ), summed in split order.
+__global__ void splitk_reduce_kernel(const float* __restrict__ partial, float* __restrict__ C,
+                                     const float* __restrict__ bias, int M, int N, int ldc,
+                                     int splits, int relu, float thr) {
+  uint64_t total = (uint64_t)M * N;
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < total; i += stride) {
+    int m = (int)(i / N);
+    int n = (int)(i % N);
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += partial[(uint64_t)s * total + i];
+    if (bias) v += bias[n];
+    if (relu && v < thr) v = thr;
+    C[(uint64_t)m * ldc + n] = v;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
+  return __uint_as_float(((unsigned)v) << 16);
+}
+
+// Reference-shaped fallback for shapes the MFMA tiles cannot take (row
+// strides or K not a multiple of the 16-byte vector): one output per thread.
+template <typename T>
+__global__ void gemm_naive_kernel(const T* A, const T* B, float* C, const float* bias, int M,
+                                  int N, int K, int lda, int ldb, int ldc, int relu, float thr) {
+  uint64_t total = (uint64_t)M * N;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int m = (int)(i / N);
+    int n = (int)(i % N);
+    float acc = 0.f;
+    for (int k = 0; k < K; ++k)
+      acc = fmaf(to_f32(A[(size_t)m * lda + k]), to_f32(B[(size_t)k * ldb + n]), acc);
+    if (bias) acc += bias[n];
+    if (relu && acc < thr) acc = thr;
+    C[(size_t)m * ldc + n] = acc;
+  }
+}
+
+template <typename T>
+__global__ void conv_naive_kernel(const T* I, const T* Wt, float* O, const float* bias, int NB,
+                                  int H, int W, int C, int F, int R, int S, int sh, int sw,
+                                  int ph, int pw, int OH, int OW, float padv, int relu,
+                                  float thr) {
+  uint64_t total = (uint64_t)NB * OH * OW * F;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+  int f = (int)(i % F);
+  int m = (int)(i / F);
+  int ow = m % OW;
+  int t = m / OW;
+  int oh = t % OH;
+  int b = t / OH;
+  float acc = 0.f;
+  for (int r = 0; r < R; ++r)
+    for (int s = 0; s < S; ++s) {
+      int ih = oh * sh + r - ph;
+      int iw = ow * sw + s - pw;
+      bool inb = ih >= 0 && ih < H && iw >= 0 && iw < W;
+      for (int c = 0; c < C; ++c) {
+        float iv = inb ? to_f32(I[(((size_t)b * H + ih) * W + iw) * C + c]) : padv;
+        acc = fmaf(iv, to_f32(Wt[(((size_t)r * S + s) * C + c) * F + f]), acc);
+      }
+    }
+  if (bias) acc += bias[f];
+  if (relu && acc < thr) acc = thr;
+  O[(size_t)m * F + f] = acc;
+  }
+}
+
+float bf16_round_host(float v) {
+  unsigned u;
+  memcpy(&u, &v, 4);
+  unsigned r = ((u >> 16) & 1u) + 0x7fffu;
+  u = ((u + r) >> 16) << 16;
+  float o;
+  memcpy(&o, &u, 4);
+  return o;
+}
+
+int grid_for(uint64_t n, int block) {
+  uint64_t g = (n + block - 1) / block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+const GemmEntry* find_entry(int dtype, int conv, const xtc_hip_tile& t) {
+  int n = 0;
+  const GemmEntry* e = gemm_registry(&n);
+  for (int i = 0; i < n; ++i) {
+    if (e[i].dtype == dtype && e[i].conv == conv && e[i].bm == t.bm && e[i].bn == t.bn &&
+        e[i].bk == t.bk && e[i].wgm == t.wgm && e[i].wgn == t.wgn)
+      return &e[i];
+  }
+  return nullptr;
+}
+
+bool has_entry(int dtype, int conv, int bm, int bn, int bk, int wgm, int wgn) {
+  xtc_hip_tile t{bm, bn, bk, wgm, wgn};
+  return find_entry(dtype, conv, t) != nullptr;
+}
+
+// Default tiles.  Chosen by shape class; tuned on MI355X with loop-explore.
+void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int* split_k) {
+  *split_k = 1;
+  auto pick = [&](int bm, int bn, int bk, int wgm, int wgn) {
+    if (has_entry(dtype, conv, bm, bn, bk, wgm, wgn)) {
+      *t = xtc_hip_tile{bm, bn, bk, wgm, wgn};
+      return true;
+    }
+    return false;
+  };
+  const bool f32 = dtype == XTC_HIP_F32;
+  const int bk = f32 ? 32 : 64;
+  if (M <= 16) {
+    // skinny: stream B once; split K until the grid fills the chip
+    int bn = 128;
+    if (pick(16, bn, bk, 1, 4) || pick(16, 64, bk, 1, 4)) {
+      int tiles = (N + t->bn - 1) / t->bn;
+      int s = 1;
+      while (tiles * s < 1024 && K / (s * 2) >= 4 * bk) s *= 2;
+      *split_k = s;
+      return;
+    }
+  }
+  if (!f32 && M >= 4096 && N >= 4096) {
+    if (pick(256, 256, 64, 2, 2)) return;
+  }
+  if (M >= 2048 && N >= 2048) {
+    if (pick(128, 128, bk, 2, 2)) return;
+  }
+  if (N <= 64) {
+    if (pick(64, 64, bk, 2, 2)) return;
+  }
+  if (pick(64, 64, bk, 2, 2)) return;
+  int n = 0;
+  const GemmEntry* e = gemm_registry(&n);
+  for (int i = 0; i < n; ++i)
+    if (e[i].dtype == dtype && e[i].conv == conv) {
+      *t = xtc_hip_tile{e[i].bm, e[i].bn, e[i].bk, e[i].wgm, e[i].wgn};
+      return;
+    }
+  *t = xtc_hip_tile{0, 0, 0, 0, 0};
+}
+
+int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m, int xcd_remap,
+                       hipStream_t s) {
+  a.tiles_m = (a.M + e->bm - 1) / e->bm;
+  a.tiles_n = (a.N + e->bn - 1) / e->bn;
+  a.group_m = group_m > 0 ? group_m : 8;
+  a.xcd_remap = xcd_remap;
+  if (split_k < 1) split_k = 1;
+  int kps = (a.K + split_k - 1) / split_k;
+  kps = (kps + e->bk - 1) / e->bk * e->bk;
+  int splits = (a.K + kps - 1) / kps;
+  a.k_per_split = kps;
+  a.partial = nullptr;
+  if (splits > 1) {
+    size_t bytes = (size_t)splits * a.M * a.N * sizeof(float);
+    a.partial = (float*)workspace(bytes);
+    if (!a.partial) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
+  }
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
+  e->launch(a, grid, s);
+  HIP_TRY(hipGetLastError());
+  if (splits > 1) {
+    uint64_t total = (uint64_t)a.M * a.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s,
+                       a.partial, a.C, a.bias, a.M, a.N, a.ldc, splits, a.relu,
+                       a.relu_threshold);
+    HIP_TRY(hipGetLastError());
+  }
+  return 0;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* xtc_hip_last_error(void) { return g_last_error.c_str(); }
+
+int xtc_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int xtc_hip_init(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail("invalid device %d", device);
+  int n = xtc_hip_device_count();
+  if (device >= n) return fail("device %d not present (%d visible)", device, n);
+  std::lock_guard<std::mutex> lk(g_mutex);
+  HIP_TRY(hipSetDevice(device));
+  DeviceState& d = g_dev[device];
+  if (!d.ready) {
+    HIP_TRY(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    d.arch = prop.gcnArchName;
+    d.name = prop.name;
+    d.ready = true;
+  }
+  g_current = device;
+  return 0;
+}
+
+static int copy_str(const std::string& s, char* buf, int len) {
+  if (!buf || len <= 0) return fail("null buffer");
+  snprintf(buf, (size_t)len, "%s", s.c_str());
+  return 0;
+}
+
+int xtc_hip_device_arch(char* buf, int len) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  return copy_str(d->arch, buf, len);
+}
+
+int xtc_hip_device_name(char* buf, int len) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  return copy_str(d->name, buf, len);
+}
+
+void* xtc_hip_stream(void) {
+  DeviceState* d = current_state();
+  return d ? (void*)d->stream : nullptr;
+}
+
+int xtc_hip_synchronize(void) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+void* xtc_hip_malloc(uint64_t bytes) {
+  if (!current_state()) {
+    fail("xtc_hip_init not called");
+    return nullptr;
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    fail("hipMalloc(%llu) failed: %s", (unsigned long long)bytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  return p;
+}
+
+int xtc_hip_free(void* ptr) {
+  if (!ptr) return 0;
+  DeviceState* d = current_state();
+  if (d) HIP_TRY(hipStreamSynchronize(d->stream));
+  HIP_TRY(hipFree(ptr));
+  return 0;
+}
+
+static int copy_sync(void* dst, const void* src, uint64_t bytes, hipMemcpyKind kind) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  if (bytes == 0) return 0;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, kind, d->stream));
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+int xtc_hip_memcpy_h2d(void* dst, const void* src, uint64_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyHostToDevice);
+}
+int xtc_hip_memcpy_d2h(void* dst, const void* src, uint64_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToHost);
+}
+int xtc_hip_memcpy_d2d(void* dst, const void* src, uint64_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+int xtc_hip_memset_zero(void* ptr, uint64_t bytes) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  if (bytes == 0) return 0;
+  if (!aligned16(ptr)) return fail("memset_zero: pointer not 16-byte aligned");
+  uint64_t n16 = bytes / 16;
+  int ntail = (int)(bytes % 16);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n16 ? n16 : 1, 256)), dim3(256), 0,
+                     d->stream, (uint4*)ptr, n16, (unsigned char*)ptr + n16 * 16, ntail);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+void* xtc_hip_event_create(void) {
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) {
+    fail("hipEventCreate failed");
+    return nullptr;
+  }
+  return (void*)e;
+}
+
+int xtc_hip_event_record(void* event, void* stream) {
+  HIP_TRY(hipEventRecord((hipEvent_t)event, pick_stream(stream)));
+  return 0;
+}
+
+int xtc_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+  HIP_TRY(hipEventSynchronize((hipEvent_t)stop));
+  HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return 0;
+}
+
+int xtc_hip_event_destroy(void* event) {
+  HIP_TRY(hipEventDestroy((hipEvent_t)event));
+  return 0;
+}
+
+int xtc_hip_gemm_instance_count(void) {
+  int n = 0;
+  gemm_registry(&n);
+  return n;
+}
+
+int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance* out) {
+  int n = 0;
+  const GemmEntry* e = gemm_registry(&n);
+  if (index < 0 || index >= n || !out) return fail("instance index %d out of range", index);
+  out->dtype = e[index].dtype;
+  out->conv = e[index].conv;
+  out->tile = xtc_hip_tile{e[index].bm, e[index].bn, e[index].bk, e[index].wgm, e[index].wgn};
+  out->lds_bytes = e[index].lds_bytes;
+  out->threads = e[index].threads;
+  return 0;
+}
+
+int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* out,
+                         int* split_k) {
+  if (!out || !split_k) return fail("null output");
+  default_tile(dtype, conv, M, N, K, out, split_k);
+  if (out->bm == 0) return fail("no kernel instance for dtype %d conv %d", dtype, conv);
+  return 0;
+}
+
+int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B, float* C,
+                   const float* bias) {
+  if (!desc) return fail("null descriptor");
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (!A || !B || !C) return fail("null operand");
+  const xtc_hip_matmul_desc& d = *desc;
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
+  const int lda = d.lda ? d.lda : d.K;
+  const int ldb = d.ldb ? d.ldb : d.N;
+  const int ldc = d.ldc ? d.ldc : d.N;
+  if (lda < d.K || ldb < d.N || ldc < d.N) return fail("leading dimension smaller than shape");
+  hipStream_t s = pick_stream(d.stream);
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 &&
+                      aligned16(A) && aligned16(B);
+  if (!vec_ok) {
+    dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
+    if (d.dtype == XTC_HIP_F32)
+      hipLaunchKernelGGL(gemm_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)A,
+                         (const float*)B, C, bias, d.M, d.N, d.K, lda, ldb, ldc, d.relu,
+                         d.relu_threshold);
+    else
+      hipLaunchKernelGGL(gemm_naive_kernel<uint16_t>, grid, dim3(128), 0, s,
+                         (const uint16_t*)A, (const uint16_t*)B, C, bias, d.M, d.N, d.K, lda,
+                         ldb, ldc, d.relu, d.relu_threshold);
+    HIP_TRY(hipGetLastError());
+    return 0;
+  }
+  xtc_hip_tile t = d.tile;
+  int split_k = d.split_k;
+  if (t.bm == 0) {
+    int sk = 1;
+    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
+    if (split_k <= 0) split_k = sk;
+  }
+  const GemmEntry* e = find_entry(d.dtype, 0, t);
+  if (!e)
+    return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
+                t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.bias = bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, s);
+}
+
+int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const void* weight,
+                   float* out, const float* bias) {
+  if (!desc) return fail("null descriptor");
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (!input || !weight || !out) return fail("null operand");
+  const xtc_hip_conv2d_desc& d = *desc;
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.N <= 0 || d.H <= 0 || d.W <= 0 || d.C <= 0 || d.F <= 0 || d.R <= 0 || d.S <= 0 ||
+      d.stride_h <= 0 || d.stride_w <= 0 || d.pad_top < 0 || d.pad_bottom < 0 ||
+      d.pad_left < 0 || d.pad_right < 0)
+    return fail("bad conv2d descriptor");
+  const int HP = d.H + d.pad_top + d.pad_bottom;
+  const int WP = d.W + d.pad_left + d.pad_right;
+  if (HP < d.R || WP < d.S) return fail("conv2d window larger than padded input");
+  const int OH = (HP - d.R) / d.stride_h + 1;
+  const int OW = (WP - d.S) / d.stride_w + 1;
+  hipStream_t s = pick_stream(d.stream);
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const int M = d.N * OH * OW;
+  const int K = d.R * d.S * d.C;
+  const bool vec_ok = d.C % vec == 0 && d.F % vec == 0 && aligned16(input) && aligned16(weight);
+  if (!vec_ok) {
+    dim3 grid(grid_for((uint64_t)M * d.F, 128));
+    if (d.dtype == XTC_HIP_F32)
+      hipLaunchKernelGGL(conv_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)input,
+                         (const float*)weight, out, bias, d.N, d.H, d.W, d.C, d.F, d.R, d.S,
+                         d.stride_h, d.stride_w, d.pad_top, d.pad_left, OH, OW, d.pad_value,
+                         d.relu, d.relu_threshold);
+    else
+      hipLaunchKernelGGL(conv_naive_kernel<uint16_t>, grid, dim3(128), 0, s,
+                         (const uint16_t*)input, (const uint16_t*)weight, out, bias, d.N, d.H,
+                         d.W, d.C, d.F, d.R, d.S, d.stride_h, d.stride_w, d.pad_top, d.pad_left,
+                         OH, OW, bf16_round_host(d.pad_value), d.relu, d.relu_threshold);
+    HIP_TRY(hipGetLastError());
+    return 0;
+  }
+  xtc_hip_tile t = d.tile;
+  int split_k = d.split_k;
+  if (t.bm == 0) {
+    int sk = 1;
+    default_tile(d.dtype, 1, M, d.F, K, &t, &sk);
+    if (split_k <= 0) split_k = sk;
+  }
+  const GemmEntry* e = find_entry(d.dtype, 1, t);
+  if (!e)
+    return fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
+                t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = input;
+  a.B = weight;
+  a.C = out;
+  a.bias = bias;
+  a.M = M;
+  a.N = d.F;
+  a.K = K;
+  a.lda = K;
+  a.ldb = d.F;
+  a.ldc = d.F;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  a.cH = d.H;
+  a.cW = d.W;
+  a.cC = d.C;
+  a.cOH = OH;
+  a.cOW = OW;
+  a.cS = d.S;
+  a.cSH = d.stride_h;
+  a.cSW = d.stride_w;
+  a.cPH = d.pad_top;
+  a.cPW = d.pad_left;
+  a.pad_value = d.pad_value;
+  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, s);
+}
+
+int xtc_hip_relu(const float* x, float* y, uint64_t n, float threshold, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (n == 0) return 0;
+  if (!x || !y) return fail("null operand");
+  if (!aligned16(x) || !aligned16(y)) return fail("relu: operands must be 16-byte aligned");
+  hipLaunchKernelGGL(relu_kernel, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0,
+                     pick_stream(stream), x, y, n, threshold);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_pad(const float* x, float* y, int ndim, const int64_t* shape, const int64_t* before,
+                const int64_t* after, float value, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (ndim < 1 || ndim > 8) return fail("pad: rank %d unsupported", ndim);
+  if (!x || !y || !shape || !before || !after) return fail("null operand");
+  PadDims d;
+  memset(&d, 0, sizeof(d));
+  d.ndim = ndim;
+  uint64_t total = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (shape[k] < 0 || before[k] < 0 || after[k] < 0) return fail("pad: negative extent");
+    d.in_shape[k] = shape[k];
+    d.before[k] = before[k];
+    d.out_shape[k] = shape[k] + before[k] + after[k];
+    total *= (uint64_t)d.out_shape[k];
+  }
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(pad_kernel, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
+                     x, y, d, total, value);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_cast_f32_to_bf16(const float* x, uint16_t* y, uint64_t n, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                     pick_stream(stream), x, y, n);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_cast_bf16_to_f32(const uint16_t* x, float* y, uint64_t n, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                     pick_stream(stream), x, y, n);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------ timing harness
+
+typedef void (*fn0)(void);
+typedef void (*fn8)(void*, void*, void*, void*, void*, void*, void*, void*);
+
+static inline void call_payload(void (*func)(void), void** args, int nargs) {
+  void* a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < nargs && i < 8; ++i) a[i] = args[i];
+  // Extra trailing arguments are ignored by the callee under the SysV ABI.
+  ((fn8)func)(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]);
+}
+
+void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_names[],
+                           int repeat, int number, int min_repeat_ms, void (*func)(void),
+                           void** args, int nargs) {
+  if (!results || repeat <= 0 || number < 0 || min_repeat_ms < 0 || !func || nargs < 0 ||
+      nargs > 8) {
+    fail("evaluate_perf: invalid arguments");
+    return;
+  }
+  // event kinds: 0 unknown, 1 gpu.time (s), 2 gpu.clocks (ns)
+  int kinds[16] = {0};
+  if (events_num > 16) events_num = 16;
+  for (int e = 0; e < events_num; ++e) {
+    const char* n = events_names[e];
+    kinds[e] = (n && !strcmp(n, "gpu.time")) ? 1 : (n && !strcmp(n, "gpu.clocks")) ? 2 : 0;
+  }
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  const bool use_events = events_num > 0 && current_state();
+  if (use_events) {
+    hipEventCreate(&ev0);
+    hipEventCreate(&ev1);
+  }
+  if (number > 0) {
+    call_payload(func, args, nargs);
+  } else {
+    number = 1;
+  }
+  for (int r = 0; r < repeat; ++r) {
+    int attempts = number;
+    double elapsed;
+    float dev_ms = 0.f;
+    while (1) {
+      if (use_events) hipEventRecord(ev0, current_state()->stream);
+      double t0 = now_s();
+      for (int a = 0; a < attempts; ++a) call_payload(func, args, nargs);
+      elapsed = now_s() - t0;
+      if (use_events) {
+        hipEventRecord(ev1, current_state()->stream);
+        hipEventSynchronize(ev1);
+        hipEventElapsedTime(&dev_ms, ev0, ev1);
+      }
+      if (elapsed * 1000.0 >= (double)min_repeat_ms) break;
+      attempts *= 2;
+    }
+    if (events_num > 0) {
+      for (int e = 0; e < events_num; ++e) {
+        double v = -1.0;
+        if (use_events && kinds[e] == 1) v = (double)dev_ms * 1e-3 / attempts;
+        if (use_events && kinds[e] == 2) v = (double)dev_ms * 1e6 / attempts;
+        results[r * events_num + e] = v;
+      }
+    } else {
+      results[r] = elapsed / attempts;
+    }
+  }
+  if (use_events) {
+    hipEventDestroy(ev0);
+    hipEventDestroy(ev1);
+  }
+}
+
+void xtc_hip_evaluate(double* results, int repeat, int number, int min_repeat_ms,
+                      void (*func)(void), void** args, int nargs) {
+  xtc_hip_evaluate_perf(results, 0, nullptr, repeat, number, min_repeat_ms, func, args, nargs);
+}
+
+double xtc_hip_evaluate_flops(const char* dtype) {
+  // Published dense MFMA peaks of MI355X (256 CUs at 2.4 GHz), in FMA/s.
+  if (!dtype) return 0.0;
+  if (!strcmp(dtype, "float32")) return 157.3e12 / 2.0;
+  if (!strcmp(dtype, "bfloat16") || !strcmp(dtype, "float16")) return 2516.6e12 / 2.0;
+  if (!strcmp(dtype, "float64")) return 78.6e12 / 2.0;
+  return 0.0;
+}
+
+}  // extern "C"
