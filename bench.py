@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+# SPDX-License-Identifier: BSD-3-Clause
+"""Headline benchmark: bf16-input / fp32-accumulate matmul M=N=K=8192 on one
+MI355X, driven through the XTC pipeline (graph -> HipBackend -> Scheduler ->
+Compiler -> payload), TFLOP/s and fraction of the dense bf16 MFMA peak.
+
+A step is one call of the compiled payload over the resident inputs (one
+GEMM launch).  Inputs are seeded uniform[-1,1) rounded to bf16 and are in HBM
+before the timed region.  The K timed calls are queued back to back and
+bracketed by HIP events on the payload's stream plus a wall clock with a
+synchronisation on both sides.
+
+Other configurations (--config C1|C2|C3b|C4|C5) print the same line for
+their own workload; the driver runs the default.  --gpus N>1 is refused:
+every box of this pool has one GPU.
+
+The cpu_baseline leg times the C restatement of XTC's llvmir CPU backend
+(oracle/, auto-scheduled over its tile variants, OpenMP on this host's cores)
+on a bounded sample of the same workload, with the reference's own
+evaluate_perf harness when oracle/_ref is built.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_TFLOPS = {"bfloat16": 2516.6, "float32": 157.3}  # dense MFMA, MI355X datasheet
+PEAK_HBM_GBS = 8000.0
+
+
+def _graph(cfg: str):  # type: ignore[no-untyped-def]
+    import xtc_amd.graphs.xtc.op as O
+
+    if cfg == "C3a":
+        a = O.tensor((8192, 8192), "bfloat16", name="A")
+        b = O.tensor((8192, 8192), "bfloat16", name="B")
+        with O.graph(name="matmul_bf16") as gb:
+            O.matmul(a, b, name="C", out_dtype="float32")
+    elif cfg == "C3b":
+        a = O.tensor((16, 8192), "bfloat16", name="A")
+        b = O.tensor((8192, 8192), "bfloat16", name="B")
+        with O.graph(name="matmul_skinny") as gb:
+            O.matmul(a, b, name="C", out_dtype="float32")
+    elif cfg in ("C1", "C2"):
+        n = 512 if cfg == "C1" else 4096
+        a = O.tensor((n, n), "float32", name="A")
+        b = O.tensor((n, n), "float32", name="B")
+        with O.graph(name="matmul") as gb:
+            O.matmul(a, b, name="C")
+    elif cfg == "C4":
+        x = O.tensor((8, 56, 56, 64), "float32", name="I")
+        w = O.tensor((3, 3, 64, 64), "float32", name="W")
+        with O.graph(name="conv_relu") as gb:
+            p = O.pad2d(x, padding=1, axes=(1, 2), name="pad")
+            c = O.conv2d(p, w, name="conv")
+            O.relu(c, name="relu")
+    elif cfg == "C5":
+        x = O.tensor((2048, 1024), "float32", name="X")
+        w1 = O.tensor((1024, 4096), "float32", name="W1")
+        w2 = O.tensor((4096, 1024), "float32", name="W2")
+        with O.graph(name="mlp") as gb:
+            h = O.relu(O.matmul(x, w1, name="fc1"), name="act")
+            O.matmul(h, w2, name="fc2")
+    else:
+        raise SystemExit(f"unknown config {cfg}")
+    return gb.graph
+
+
+# Tuned schedules, expressed with XTC's scheduling primitives: the first tile
+# level of i/j is the workgroup tile, the second the wave tile, k's first
+# level the LDS slab (xtc_amd/backends/hip/mapping.py).
+SCHEDULES = {
+    "C3a": {"C": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 256, "j2": 128}, "k": {"k1": 64}}},
+    "C2": {"C": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 16}}},
+}
+
+
+def _inputs(cfg: str, graph) -> list[np.ndarray]:  # type: ignore[no-untyped-def]
+    """Seeded inputs of the BASELINE configuration: one default_rng(0), drawn
+    in graph input order in float64, cast (bf16: rounded)."""
+    from xtc_amd.utils.bf16 import round_to_bf16
+
+    rng = np.random.default_rng(0)
+    out = []
+    for t in graph.inputs_types:
+        shape = tuple(t.constant_shape)
+        if cfg == "C4" and len(shape) == 4 and shape[0] == 3:
+            arr = rng.normal(0.0, np.sqrt(2.0 / (9 * 64)), size=shape)
+        elif cfg == "C4":
+            arr = rng.uniform(0.0, 1.0, size=shape)
+        elif cfg == "C5" and shape != (2048, 1024):
+            arr = rng.normal(0.0, 0.02, size=shape)
+        else:
+            arr = rng.uniform(-1.0, 1.0, size=shape)
+        arr = arr.astype(np.float32)
+        out.append(round_to_bf16(arr) if t.constant_dtype == "bfloat16" else arr)
+    return out
+
+
+def _flops(cfg: str) -> int:
+    return {
+        "C1": 2 * 512**3,
+        "C2": 2 * 4096**3,
+        "C3a": 2 * 8192**3,
+        "C3b": 2 * 16 * 8192 * 8192,
+        "C4": 2 * 8 * 56 * 56 * 64 * 576,
+        "C5": 2 * 2048 * 4096 * 1024 * 2,
+    }[cfg]
+
+
+def _alg_bytes(cfg: str) -> int:
+    return {
+        "C1": 3 * 512 * 512 * 4,
+        "C2": 3 * 4096 * 4096 * 4,
+        "C3a": 2 * 8192 * 8192 * 2 + 8192 * 8192 * 4,
+        "C3b": 16 * 8192 * 2 + 8192 * 8192 * 2 + 16 * 8192 * 4,
+        "C4": 8 * 56 * 56 * 64 * 4 * 2 + 9 * 64 * 64 * 4,
+        "C5": (2048 * 1024 + 1024 * 4096 + 2 * 2048 * 4096 + 4096 * 1024 + 2048 * 1024) * 4,
+    }[cfg]
+
+
+def _traffic(cfg: str) -> float | None:
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = ROOT / "profiles" / f"traffic_{cfg}.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def _cpu_baseline(cfg: str) -> dict:
+    """Times the CPU restatement on a bounded sample of the workload."""
+    from oracle import cpu_baseline as cb
+    from xtc_amd.utils.bf16 import round_to_bf16
+
+    n = 2048 if cfg in ("C3a", "C2", "C5") else 512
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    if cfg.startswith("C3"):
+        a, b = round_to_bf16(a), round_to_bf16(b)
+    cores = cb.threads()
+    variant, _ = cb.autoschedule_matmul(a, b, repeat=1, min_repeat_ms=50)
+    t = cb.time_matmul(a, b, variant, repeat=3, min_repeat_ms=200)
+    tiles = cb.variants()[variant]
+    harness = "reference evaluate_perf" if cb.ref_runtime() is not None else "evaluate_perf protocol (Python)"
+    return {
+        "value": round(2 * n**3 / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (
+            f"fp32 matmul {n}x{n}x{n} (inputs like {cfg}{', bf16-rounded' if cfg.startswith('C3') else ''}), "
+            f"XTC llvmir restatement (tile_oo order i,k,j,i1,k1,j1; best tiles i1,k1,j1={tiles} of "
+            f"{len(cb.variants())} auto-scheduled), OpenMP {cores} threads, {harness}, CPU: {cb.cpu_model()}"
+        ),
+    }
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C3a", choices=["C1", "C2", "C3a", "C3b", "C4", "C5"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: every box of this pool has one GPU; "
+            "the kernel is measured on one GPU's share (see DESIGN.md for how it would shard).",
+            file=sys.stderr,
+        )
+        return 2
+
+    from xtc_amd.backends.hip import Backend
+    from xtc_amd.runtimes.hip import capi
+    from xtc_amd.runtimes.hip.device import HipDevice
+    from xtc_amd.runtimes.hip.ndarray import DeviceArray
+
+    cfg = args.config
+    graph = _graph(cfg)
+    backend = Backend(graph)
+    sch = backend.get_scheduler()
+    for node, dims in SCHEDULES.get(cfg, {}).items():
+        sch = backend.get_scheduler(default_node=node)
+        for dim, tiles in dims.items():
+            sch.tile(dim, tiles)
+    module = backend.get_compiler(synchronize=False, schedule_policy="strict").compile(sch.schedule())
+
+    dev = HipDevice(0)
+    dev.init_device()
+    dev.load_module(module)
+    fn = dev.get_module_function(module, module.payload_name)
+    fn.restype = None
+    status = dev.module_symbol(module, f"{module.payload_name}_status")
+    status.restype = ctypes.c_int
+
+    host_in = _inputs(cfg, graph)
+    d_in = [DeviceArray.from_numpy(a, t.constant_dtype, dev) for a, t in zip(host_in, graph.inputs_types)]
+    d_out = [DeviceArray(t.constant_shape, t.constant_dtype, dev) for t in graph.outputs_types]
+    cargs = [ctypes.c_void_p(d.data) for d in (*d_in, *d_out)]
+
+    def step() -> None:
+        fn(*cargs)
+
+    L = capi.lib()
+    # parity spot check of the bench's own output (rows 0..7) in float64
+    step()
+    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    if status():
+        raise SystemExit(f"payload failed: {dev.module_symbol(module, f'{module.payload_name}_message')()}")
+    spot_err = None
+    if cfg in ("C3a", "C3b", "C1", "C2"):
+        out = d_out[0].numpy()
+        a64, b64 = host_in[0][:8].astype(np.float64), host_in[1].astype(np.float64)
+        ref = a64 @ b64
+        k = host_in[0].shape[1]
+        spot_err = float(np.abs(out[:8] - ref).max() / (np.sqrt(k) * np.abs(host_in[0]).max() * np.abs(host_in[1]).max()))
+        tol = 1e-2 if cfg.startswith("C3") else 1e-4
+        if not spot_err <= tol:
+            raise SystemExit(f"parity spot check failed: scaled error {spot_err} > {tol}")
+
+    for _ in range(args.warmup):
+        step()
+    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    e0, e1 = L.xtc_hip_event_create(), L.xtc_hip_event_create()
+    capi.check(L.xtc_hip_event_record(e0, None), "event")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    capi.check(L.xtc_hip_event_record(e1, None), "event")
+    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    wall = time.perf_counter() - t0
+    ms = ctypes.c_float()
+    capi.check(L.xtc_hip_event_elapsed_ms(e0, e1, ctypes.byref(ms)), "elapsed")
+    if status():
+        raise SystemExit("payload reported an error during the timed region")
+    kernel_s = ms.value * 1e-3 / args.steps
+    step_s = wall / args.steps
+    flops = _flops(cfg)
+    dtype = graph.inputs_types[0].constant_dtype
+    conf = next(iter(module.configs.values()), None)
+    if cfg == "C3b":
+        achieved = _alg_bytes(cfg) / kernel_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    else:
+        achieved = flops / kernel_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS[dtype], "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = _traffic(cfg)
+    line = {
+        "metric": "TFLOP/s + % of MFMA peak, matmul/conv2d on 1 MI355X vs MLIR-CPU baseline",
+        "value": round(flops / step_s / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bfloat16": "bf16 in, fp32 acc/out", "float32": "fp32"}[dtype],
+        "data": "synthetic: seeded uniform/normal inputs of the BASELINE config",
+        "config": {
+            "workload": cfg,
+            "graph": str(graph.name),
+            "flop_per_step": flops,
+            "kernel": conf.describe() if conf else None,
+            "kernel_ms": round(kernel_s * 1e3, 4),
+            "pct_of_peak": round(100 * roof["frac"], 2),
+            "parity_spot_scaled_err": spot_err,
+        },
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        try:
+            line["cpu_baseline"] = _cpu_baseline(cfg)
+        except Exception as err:  # the GPU figure stands without it
+            line["cpu_baseline"] = {"value": None, "error": str(err)}
+    print(json.dumps(line), flush=True)
+    for d in (*d_in, *d_out):
+        d.free()
+    dev.unload_module(module)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,211 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""TEST INFRASTRUCTURE: driver of the CPU baseline (oracle/cpu_backend.c).
+
+Builds the C restatement of XTC's `llvmir` CPU backend for the host it runs
+on (-march=native must match the machine, so the object is built per host),
+auto-schedules it by timing every compiled tile variant, and times the best
+one with the reference's evaluate_perf protocol: one warm-up call, then per
+repeat a call count doubling until the batch lasts min_repeat_ms, result =
+batch time / calls, min over repeats
+(src/xtc/csrcs/runtimes/host/evaluate_perf.c:63-125).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import platform
+import subprocess
+import time
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+SRC = HERE / "cpu_backend.c"
+
+__all__ = [
+    "load",
+    "threads",
+    "matmul",
+    "conv2d",
+    "time_matmul",
+    "autoschedule_matmul",
+    "cpu_model",
+    "ref_runtime",
+    "ref_peak_flops",
+]
+
+REF_RUNTIME = HERE / "_ref" / "libxtc_ref_runtime.so"
+_ref: ctypes.CDLL | None = None
+
+
+def ref_runtime() -> ctypes.CDLL | None:
+    """The reference's own host runtime built by `make -C oracle ref`
+    (evaluate_perf, evaluate_flops), or None when it was not built."""
+    global _ref
+    if _ref is None and REF_RUNTIME.exists():
+        h = ctypes.CDLL(str(REF_RUNTIME))
+        h.evaluate_perf.argtypes = [
+            ctypes.POINTER(ctypes.c_double),
+            ctypes.c_int,
+            ctypes.POINTER(ctypes.c_char_p),
+            ctypes.c_int,
+            ctypes.c_int,
+            ctypes.c_int,
+            ctypes.c_void_p,
+            ctypes.POINTER(ctypes.c_void_p),
+            ctypes.c_int,
+        ]
+        h.evaluate_perf.restype = None
+        h.evaluate_flops.argtypes = [ctypes.c_char_p]
+        h.evaluate_flops.restype = ctypes.c_double
+        _ref = h
+    return _ref
+
+
+def ref_peak_flops(dtype: str = "float32") -> float | None:
+    """Single-core FMA/s peak from the reference's evaluate_flops
+    (src/xtc/csrcs/runtimes/host/evaluate_flops.c:461-494)."""
+    h = ref_runtime()
+    return None if h is None else float(h.evaluate_flops(dtype.encode()))
+
+_lib: ctypes.CDLL | None = None
+
+
+def _host_key() -> str:
+    info = platform.node() + platform.machine() + cpu_model()
+    return hashlib.sha256((info + SRC.read_text()).encode()).hexdigest()[:12]
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def load() -> ctypes.CDLL:
+    """Builds (once per host) and loads libxtc_cpu.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    out_dir = HERE / "_build" / _host_key()
+    lib = out_dir / "libxtc_cpu.so"
+    if not lib.exists():
+        out_dir.mkdir(parents=True, exist_ok=True)
+        cc = os.environ.get("CC", "gcc")
+        tmp = lib.with_suffix(f".so.tmp{os.getpid()}")
+        cmd = [cc, "-O3", "-march=native", "-ffp-contract=fast", "-fopenmp", "-fPIC", "-std=c11",
+               "-shared", "-o", str(tmp), str(SRC)]
+        subprocess.run(cmd, check=True, capture_output=True)
+        os.replace(tmp, lib)
+    handle = ctypes.CDLL(str(lib))
+    fp = ctypes.POINTER(ctypes.c_float)
+    handle.xtc_cpu_matmul.argtypes = [ctypes.c_int, fp, fp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    handle.xtc_cpu_matmul.restype = ctypes.c_int
+    handle.xtc_cpu_conv2d.argtypes = [fp, fp, fp] + [ctypes.c_int] * 10
+    handle.xtc_cpu_conv2d.restype = ctypes.c_int
+    handle.xtc_cpu_matmul_variant_tiles.argtypes = [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 3
+    handle.xtc_cpu_set_threads.argtypes = [ctypes.c_int]
+    handle.xtc_cpu_configure_matmul.argtypes = [ctypes.c_int] * 4
+    _lib = handle
+    return handle
+
+
+def threads(n: int | None = None) -> int:
+    lib = load()
+    if n:
+        lib.xtc_cpu_set_threads(int(n))
+    return int(lib.xtc_cpu_threads())
+
+
+def variants() -> list[tuple[int, int, int]]:
+    lib = load()
+    out = []
+    for v in range(lib.xtc_cpu_matmul_variants()):
+        ti, tk, tj = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        lib.xtc_cpu_matmul_variant_tiles(v, ctypes.byref(ti), ctypes.byref(tk), ctypes.byref(tj))
+        out.append((ti.value, tk.value, tj.value))
+    return out
+
+
+def _fp(a: np.ndarray) -> "ctypes._Pointer[ctypes.c_float]":
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def matmul(a: np.ndarray, b: np.ndarray, variant: int = 0) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    if load().xtc_cpu_matmul(variant, _fp(a), _fp(b), _fp(c), m, n, k):
+        raise ValueError("xtc_cpu_matmul rejected its arguments")
+    return c
+
+
+def conv2d(x_padded: np.ndarray, w: np.ndarray, stride: tuple[int, int] = (1, 1), relu: bool = False) -> np.ndarray:
+    x = np.ascontiguousarray(x_padded, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    nb, h, wd, c = x.shape
+    r, s, _, f = w.shape
+    oh, ow = (h - r) // stride[0] + 1, (wd - s) // stride[1] + 1
+    o = np.empty((nb, oh, ow, f), np.float32)
+    if load().xtc_cpu_conv2d(_fp(x), _fp(w), _fp(o), nb, h, wd, c, f, r, s, stride[0], stride[1], int(relu)):
+        raise ValueError("xtc_cpu_conv2d rejected its arguments")
+    return o
+
+
+def time_call(fn, repeat: int = 3, min_repeat_ms: int = 100) -> float:  # type: ignore[no-untyped-def]
+    """evaluate_perf protocol; returns min over repeats of seconds per call."""
+    fn()
+    best = float("inf")
+    for _ in range(repeat):
+        calls = 1
+        while True:
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn()
+            dt = time.perf_counter() - t0
+            if dt * 1000.0 >= min_repeat_ms:
+                break
+            calls *= 2
+        best = min(best, dt / calls)
+    return best
+
+
+def time_matmul(a: np.ndarray, b: np.ndarray, variant: int, repeat: int = 3, min_repeat_ms: int = 100) -> float:
+    """Seconds per call of one variant, min over repeats.  Uses the
+    reference's own evaluate_perf when oracle/_ref is built, else the same
+    protocol restated in Python."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib = load()
+    ref = ref_runtime()
+    if ref is not None:
+        if lib.xtc_cpu_configure_matmul(variant, m, n, k):
+            raise ValueError("bad matmul configuration")
+        results = (ctypes.c_double * repeat)()
+        args = (ctypes.c_void_p * 3)(a.ctypes.data, b.ctypes.data, c.ctypes.data)
+        fn = ctypes.cast(lib.xtc_cpu_matmul_payload, ctypes.c_void_p)
+        ref.evaluate_perf(results, 0, None, repeat, 1, min_repeat_ms, fn, args, 3)
+        return float(min(results))
+    pa, pb, pc = _fp(a), _fp(b), _fp(c)
+    return time_call(lambda: lib.xtc_cpu_matmul(variant, pa, pb, pc, m, n, k), repeat, min_repeat_ms)
+
+
+def autoschedule_matmul(a: np.ndarray, b: np.ndarray, repeat: int = 2, min_repeat_ms: int = 50) -> tuple[int, float]:
+    """Times every tile variant; returns (best variant, its seconds per call)."""
+    results = [(time_matmul(a, b, v, repeat, min_repeat_ms), v) for v in range(len(variants()))]
+    t, v = min(results)
+    return v, t

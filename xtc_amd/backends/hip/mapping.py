@@ -1,0 +1,199 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""Schedule -> GEMM kernel template parameters.
+
+A matmul/conv2d launch runs one instance of the MFMA GEMM template
+(xtc_amd/csrc/gemm.hpp): a workgroup computes a BM x BN output tile with
+WGM x WGN waves, walking K in BK slabs through LDS.  XTC's loop knobs map
+onto it as follows (dims of matmul: i, j, k; of conv2d: b, h, w, f, r, s, c,
+where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
+
+  * first tile level of the M dims   -> BM (product over b,h,w for conv)
+  * first tile level of the N dim    -> BN
+  * second tile level of M / N       -> wave tile WM / WN, so WGM = BM/WM,
+                                        WGN = BN/WN (absent: library choice)
+  * first tile level of the K dims   -> BK (LDS slab depth)
+  * parallelize(k)                   -> split-K: K / (first k level) slices
+                                        reduced by a second kernel; BK is then
+                                        the second k level
+  * interchange with N's base loop outside M's -> column-major tile raster;
+    otherwise tiles are rastered in groups of 8 tile-rows (L2 reuse)
+  * vectorize, unroll, pack_at(local), buffer_at, fuse_producer_at -> always
+    on in these kernels (16-byte vector loads, fully unrolled MFMA loops,
+    LDS staging of both operands, register-resident output tile, pad folded
+    into the conv loader); recorded, no further effect.
+
+Tile semantics follow the reference: a tile size is the extent of the
+sub-loop (src/xtc/backends/mlir/MlirCompilerPasses.py:414-457).
+
+A request that matches no compiled instance is either rejected
+(policy "strict") or mapped to the nearest instance in log2 distance
+(policy "nearest", the default); the result records which happened.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from functools import lru_cache
+from math import prod
+from typing import Any
+
+from .scheduler import HipNodeSchedule, ScheduleError
+
+__all__ = ["GemmConfig", "map_gemm", "gemm_instances", "legal_tiles"]
+
+DEFAULT_GROUP_M = 8
+
+
+@dataclass(frozen=True)
+class GemmConfig:
+    dtype: str
+    conv: bool
+    bm: int
+    bn: int
+    bk: int
+    wgm: int
+    wgn: int
+    split_k: int = 1
+    group_m: int = DEFAULT_GROUP_M
+    xcd_remap: int = 1
+    exact: bool = True
+    source: str = "schedule"  # "schedule" | "nearest" | "default"
+
+    @property
+    def tile(self) -> tuple[int, int, int, int, int]:
+        return (self.bm, self.bn, self.bk, self.wgm, self.wgn)
+
+    def describe(self) -> str:
+        return (
+            f"{'conv' if self.conv else 'gemm'}<{self.dtype}> BMxBNxBK={self.bm}x{self.bn}x{self.bk} "
+            f"waves={self.wgm}x{self.wgn} split_k={self.split_k} group_m={self.group_m} ({self.source})"
+        )
+
+
+@lru_cache(maxsize=None)
+def gemm_instances() -> tuple[tuple[str, bool, tuple[int, int, int, int, int]], ...]:
+    """(dtype, conv, tile) of every kernel instance compiled into libxtc_hip."""
+    from ...runtimes.hip import capi
+
+    return tuple((i["dtype"], bool(i["conv"]), tuple(i["tile"])) for i in capi.gemm_instances())  # type: ignore[misc]
+
+
+def legal_tiles(dtype: str, conv: bool) -> list[tuple[int, int, int, int, int]]:
+    return [t for d, c, t in gemm_instances() if d == dtype and c == conv]
+
+
+def _dims_roles(sched: HipNodeSchedule, conv: bool) -> tuple[list[str], list[str], list[str]]:
+    d = sched.dims
+    if conv:
+        return d[0:3], [d[3]], d[4:7]
+    return [d[0]], [d[1]], [d[2]]
+
+
+def _level(sched: HipNodeSchedule, dims: list[str], level: int) -> int | None:
+    """Product over `dims` of the tile extent at `level` (a dim with fewer
+    levels contributes its innermost extent, an untiled dim 1); None if no
+    dim reaches that level."""
+    if not any(len(sched.levels(d)) > level for d in dims):
+        return None
+    out = 1
+    for d in dims:
+        lv = sched.levels(d)
+        out *= lv[min(level, len(lv) - 1)] if lv else 1
+    return out
+
+
+def _default(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int], int]:
+    from ...runtimes.hip import capi
+
+    return capi.default_tile(dtype, conv, M, N, K)
+
+
+def _nearest(req: dict[str, int | None], cands: list[tuple[int, int, int, int, int]]) -> tuple[int, int, int, int, int]:
+    def cost(t: tuple[int, int, int, int, int]) -> tuple[float, int]:
+        bm, bn, bk, wgm, wgn = t
+        have = {"bm": bm, "bn": bn, "bk": bk, "wm": bm // wgm, "wn": bn // wgn}
+        c = 0.0
+        for k, v in req.items():
+            if v:
+                c += abs(math.log2(have[k]) - math.log2(v))
+        return (c, -(wgm * wgn))
+
+    return min(cands, key=cost)
+
+
+def map_gemm(
+    launch_attrs: dict[str, Any],
+    conv: bool,
+    sched: HipNodeSchedule | None,
+    policy: str = "nearest",
+) -> GemmConfig:
+    dtype = launch_attrs["dtype"]
+    M, N, K = launch_attrs["M"], launch_attrs["N"], launch_attrs["K"]
+    cands = legal_tiles(dtype, conv)
+    if not cands:
+        raise ScheduleError(f"no compiled {'conv' if conv else 'matmul'} instance for {dtype}")
+    if sched is None or not any(sched.levels(d) for d in sched.dims) and not sched.parallelization:
+        tile, split = _default(dtype, conv, M, N, K)
+        return GemmConfig(dtype, conv, *tile, split_k=split, exact=True, source="default")
+    if sched.splits:
+        raise ScheduleError(f"{sched.node_name}: split() has no HIP kernel mapping")
+    m_dims, n_dims, k_dims = _dims_roles(sched, conv)
+    bm = _level(sched, m_dims, 0)
+    bn = _level(sched, n_dims, 0)
+    wm = _level(sched, m_dims, 1)
+    wn = _level(sched, n_dims, 1)
+    k_parallel = any(sched.is_parallel(d) for d in k_dims)
+    split_k = 1
+    if k_parallel:
+        kslice = _level(sched, k_dims, 0)
+        if kslice is None:
+            raise ScheduleError(f"{sched.node_name}: parallelize on K needs a K tile (the slice per split)")
+        if K % kslice:
+            raise ScheduleError(f"{sched.node_name}: K={K} is not a multiple of the split-K slice {kslice}")
+        split_k = K // kslice
+        bk = _level(sched, k_dims, 1)
+    else:
+        bk = _level(sched, k_dims, 0)
+    order = sched.base_order()
+    col_major = bool(order) and order.index(n_dims[0]) < min(order.index(d) for d in m_dims if d in order)
+    group_m = (M + (bm or 64) - 1) // (bm or 64) if col_major else DEFAULT_GROUP_M
+
+    dflt_tile, dflt_split = _default(dtype, conv, M, N, K)
+    req_bm = bm or dflt_tile[0]
+    req_bn = bn or dflt_tile[1]
+    req_bk = bk or dflt_tile[2]
+    matches = [
+        t
+        for t in cands
+        if t[0] == req_bm
+        and t[1] == req_bn
+        and t[2] == req_bk
+        and (wm is None or t[0] // t[3] == wm)
+        and (wn is None or t[1] // t[4] == wn)
+    ]
+    if matches:
+        # unspecified wave split: the instance with the most waves
+        tile = max(matches, key=lambda t: (t[3] * t[4], t[3]))
+        return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=True, source="schedule")
+    if policy == "strict":
+        wave = "" if wm is None and wn is None else f" wave tile {wm}x{wn}"
+        raise ScheduleError(
+            f"{sched.node_name}: no {dtype} {'conv' if conv else 'matmul'} kernel for block tile "
+            f"{req_bm}x{req_bn}x{req_bk}{wave}; compiled tiles (BM,BN,BK,WGM,WGN): "
+            f"{sorted(set(cands))[:12]}..."
+        )
+    tile = _nearest({"bm": req_bm, "bn": req_bn, "bk": req_bk, "wm": wm, "wn": wn}, cands)
+    return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=False, source="nearest")
+
+
+def schedule_is_legal(sched: HipNodeSchedule, launch_attrs: dict[str, Any], conv: bool) -> bool:
+    """True if `sched` maps exactly onto a compiled instance."""
+    try:
+        return map_gemm(launch_attrs, conv, sched, policy="strict").exact
+    except ScheduleError:
+        return False
+
+
+def gemm_flops(attrs: dict[str, Any]) -> int:
+    return 2 * prod((attrs["M"], attrs["N"], attrs["K"]))

@@ -1,0 +1,290 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""Scheduler of the HIP backend.
+
+Same surface and recording semantics as the reference's MLIR scheduler
+(src/xtc/backends/mlir/MlirScheduler.py:21-288,
+src/xtc/backends/mlir/MlirNodeScheduler.py:17-232): one node scheduler per
+operator node, transformations recorded under loop names "<root>/<name>",
+the default interchange being the base dims then tile levels, and
+`get_scheduler(default_node=..., nodes=...)` selecting the target node.
+Where the MLIR backend defaults to the last node, this backend defaults to
+the node whose kernel produces the graph output (a relu fused into a matmul
+epilogue is not a kernel of its own).
+
+The recorded schedule is turned into kernel template parameters by
+`mapping.py` at compile time.
+"""
+
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass, field
+from pprint import pformat
+from typing import TYPE_CHECKING, Any
+
+from ...itf.schd import DEFAULT_ROOT, Schedule, Scheduler
+from ...schedules.loop_nest import LoopNest, LoopNestNode, SplitOrigin
+
+if TYPE_CHECKING:
+    from .backend import HipBackend
+
+__all__ = ["HipScheduler", "HipSchedule", "HipNodeSchedule", "ScheduleError"]
+
+_SEP = "/"
+
+
+class ScheduleError(ValueError):
+    """A transformation the HIP backend cannot express."""
+
+
+def loop_name(root: str, name: str) -> str:
+    return f"{root}{_SEP}{name}"
+
+
+def basename(name: str) -> str:
+    return name.split(_SEP)[-1]
+
+
+@dataclass(frozen=True)
+class HipNodeSchedule:
+    node_name: str
+    dims: list[str]
+    sizes: dict[str, int]
+    splits: dict[str, dict[str, int]]
+    tiles: dict[str, dict[str, int]]
+    permutation: dict[str, list[str]]
+    vectorization: list[str]
+    parallelization: list[str]
+    unrolling: dict[str, int]
+    packed_buffers: dict[str, list[int]]
+    buffers: list[str]
+    fused: list[tuple[str, int]]
+
+    def levels(self, dim: str) -> list[int]:
+        """Tile extents of `dim`, outer to inner (empty if untiled)."""
+        return list(self.tiles.get(dim, {}).values())
+
+    def base_order(self, root: str = DEFAULT_ROOT) -> list[str]:
+        """Base dims in the order they appear in the root's permutation."""
+        perm = [basename(p) for p in self.permutation.get(root, [])]
+        return [p for p in perm if p in self.dims]
+
+    def is_parallel(self, dim: str, root: str = DEFAULT_ROOT) -> bool:
+        return loop_name(root, dim) in self.parallelization
+
+    def __str__(self) -> str:
+        return pformat(asdict(self), sort_dicts=False)
+
+
+class _NodeScheduler:
+    def __init__(self, node_name: str, dims: list[str], sizes: dict[str, int]) -> None:
+        self.node_name = node_name
+        self.dims = list(dims)
+        self.sizes = dict(sizes)
+        self.splits: dict[str, dict[str, int]] = {}
+        self.tiles: dict[str, dict[str, int]] = {d: {} for d in self.dims}
+        self.permutation: dict[str, list[str]] = {}
+        self.vectorization: list[str] = []
+        self.parallelization: list[str] = []
+        self.unrolling: dict[str, int] = {}
+        self.packed_buffers: dict[str, list[int]] = {}
+        self.buffers: list[str] = []
+        self.fused: list[tuple[str, int]] = []
+
+    def _dim_of(self, name: str) -> str:
+        if name in self.dims:
+            return name
+        for d, lv in self.tiles.items():
+            if name in lv:
+                return d
+        raise ScheduleError(f"{self.node_name}: unknown loop {name!r}")
+
+    def default_interchange(self, root: str) -> list[str]:
+        order = [loop_name(root, d) for d in self.dims]
+        depth = max((len(v) for v in self.tiles.values()), default=0)
+        for lvl in range(depth):
+            for d in self.dims:
+                names = list(self.tiles.get(d, {}))
+                if lvl < len(names):
+                    order.append(loop_name(root, names[lvl]))
+        return order
+
+    def freeze(self) -> HipNodeSchedule:
+        if not self.permutation:
+            self.permutation[DEFAULT_ROOT] = self.default_interchange(DEFAULT_ROOT)
+        return HipNodeSchedule(
+            node_name=self.node_name,
+            dims=list(self.dims),
+            sizes=dict(self.sizes),
+            splits={k: dict(v) for k, v in self.splits.items()},
+            tiles={k: {basename(n): s for n, s in v.items()} for k, v in self.tiles.items() if k in self.dims},
+            permutation={k: list(v) for k, v in self.permutation.items()},
+            vectorization=list(self.vectorization),
+            parallelization=list(self.parallelization),
+            unrolling=dict(self.unrolling),
+            packed_buffers={k: list(v) for k, v in self.packed_buffers.items()},
+            buffers=list(self.buffers),
+            fused=list(self.fused),
+        )
+
+
+class HipScheduler(Scheduler):
+    def __init__(
+        self,
+        backend: "HipBackend",
+        nodes: list[str] | None = None,
+        default_node: str | None = None,
+    ) -> None:
+        self._backend = backend
+        names = nodes if nodes is not None else backend.node_names
+        self._schedulers: dict[str, _NodeScheduler] = {}
+        for name in names:
+            op = backend.node_operation(name)
+            dims = list(op.dims)
+            self._schedulers[name] = _NodeScheduler(name, dims, {d: int(v) for d, v in op.dims.items()})
+        target = default_node if default_node is not None else backend.default_node
+        if target not in self._schedulers:
+            raise ScheduleError(f"no schedulable node named {target!r} (nodes: {list(self._schedulers)})")
+        self._current = self._schedulers[target]
+
+    @property
+    def backend(self) -> "HipBackend":
+        return self._backend
+
+    @property
+    def node_name(self) -> str:
+        return self._current.node_name
+
+    def schedule(self) -> "HipSchedule":
+        return HipSchedule(self, [s.freeze() for s in self._schedulers.values()])
+
+    def set_dims(self, dims: list[str]) -> None:
+        cur = self._current
+        if len(dims) != len(cur.dims):
+            raise ScheduleError(f"set_dims: {len(dims)} names for {len(cur.dims)} dims")
+        cur.sizes = {new: cur.sizes[old] for new, old in zip(dims, cur.dims)}
+        cur.dims = list(dims)
+        cur.tiles = {d: {} for d in cur.dims}
+
+    def split(self, dim: str, segments: dict[str, int], root: str = DEFAULT_ROOT) -> None:
+        cur = self._current
+        cur._dim_of(dim)
+        renamed = {loop_name(root, k): int(v) for k, v in segments.items()}
+        cur.splits[dim] = renamed
+        for seg in renamed:
+            cur.tiles.setdefault(seg, {})
+
+    def tile(self, dim: str, tiles: dict[str, int], root: str = DEFAULT_ROOT) -> None:
+        cur = self._current
+        if dim not in cur.tiles:
+            raise ScheduleError(f"{cur.node_name}: cannot tile unknown dim {dim!r} (dims: {cur.dims})")
+        for name, size in tiles.items():
+            if int(size) <= 0:
+                raise ScheduleError(f"{cur.node_name}: tile {name}={size} must be positive")
+            cur.tiles[dim][loop_name(root, name)] = int(size)
+
+    def interchange(self, permutation: list[str], root: str = DEFAULT_ROOT) -> None:
+        self._current.permutation[root] = [loop_name(root, a) for a in permutation]
+
+    def vectorize(self, axes: list[str], root: str = DEFAULT_ROOT) -> None:
+        self._current.vectorization += [loop_name(root, a) for a in axes]
+
+    def parallelize(self, axes: list[str], root: str = DEFAULT_ROOT) -> None:
+        self._current.parallelization = [loop_name(root, a) for a in axes]
+
+    def unroll(self, unrolls: dict[str, int], root: str = DEFAULT_ROOT) -> None:
+        for name, factor in unrolls.items():
+            self._current.unrolling[loop_name(root, name)] = int(factor)
+
+    def buffer_at(self, axis: str, mtype: str | None = None, root: str = DEFAULT_ROOT) -> None:
+        if mtype not in (None, "global", "local"):
+            raise ScheduleError(f"buffer_at: unknown memory type {mtype!r}")
+        self._current.buffers.append(loop_name(root, axis))
+
+    def pack_at(
+        self,
+        axis: str,
+        input_idx: int,
+        mtype: str | None = None,
+        pad: bool = False,
+        root: str = DEFAULT_ROOT,
+    ) -> None:
+        if mtype not in (None, "global", "local"):
+            raise ScheduleError(f"pack_at: unknown memory type {mtype!r}")
+        self._current.packed_buffers.setdefault(loop_name(root, axis), []).append(int(input_idx))
+
+    def fuse_producer_at(self, axis: str, input_idx: int, root: str = DEFAULT_ROOT) -> None:
+        self._current.fused.append((loop_name(root, axis), int(input_idx)))
+
+    def _single_gpu(self, what: str) -> None:
+        raise ScheduleError(
+            f"{what}: the HIP backend runs one kernel on one GPU per process; "
+            "multi-device meshes are not supported"
+        )
+
+    def define_memory_mesh(self, axes: dict[str, int]) -> None:
+        self._single_gpu("define_memory_mesh")
+
+    def define_processor_mesh(self, axes: dict[str, int]) -> None:
+        self._single_gpu("define_processor_mesh")
+
+    def distribute(self, axis: str, processor_axis: str, root: str = DEFAULT_ROOT) -> None:
+        self._single_gpu("distribute")
+
+    def distributed_buffer_at(
+        self, axis: str, input_idx: int, memory_axes: list[str], root: str = DEFAULT_ROOT
+    ) -> None:
+        self._single_gpu("distributed_buffer_at")
+
+    def get_loop_nest(self) -> LoopNest:
+        sched = self._current.freeze()
+        nest = LoopNest(abstract_dims=list(sched.dims), sizes=dict(sched.sizes))
+        root = nest.build_root_node(sched.node_name)
+        for dim, segs in sched.splits.items():
+            root.splits[dim] = {basename(k): v for k, v in segs.items()}
+        seg_origin: dict[str, SplitOrigin] = {}
+        for dim, segs in sched.splits.items():
+            names = list(segs)
+            for idx, seg in enumerate(names):
+                end = segs[names[idx + 1]] if idx + 1 < len(names) else None
+                seg_origin[basename(seg)] = SplitOrigin(axis=dim, start=segs[seg], end=end)
+
+        def fill(node: LoopNestNode, perm: list[str]) -> None:
+            members = set(perm)
+            node.interchange = [basename(p) for p in perm]
+            for dim, levels in self._current.tiles.items():
+                for name, size in levels.items():
+                    if name in members:
+                        node.tiles.setdefault(dim, {})[basename(name)] = size
+            node.vectorize = [basename(v) for v in sched.vectorization if v in members]
+            node.parallelize = [basename(p) for p in sched.parallelization if p in members]
+            node.unroll = {basename(k): v for k, v in sched.unrolling.items() if k in members}
+
+        for r, perm in sched.permutation.items():
+            name = basename(r)
+            if name in seg_origin:
+                child = LoopNestNode(root=name, tiles={d: {} for d in sched.dims}, split_origin=seg_origin[name])
+                fill(child, perm)
+                root.add_child(child)
+            else:
+                fill(root, perm)
+        return nest
+
+
+class HipSchedule(Schedule):
+    def __init__(self, scheduler: HipScheduler, nodes_schedules: list[HipNodeSchedule]) -> None:
+        self._scheduler = scheduler
+        self._nodes = {s.node_name: s for s in nodes_schedules}
+
+    @property
+    def scheduler(self) -> HipScheduler:
+        return self._scheduler
+
+    @property
+    def schedule_impl(self) -> list[HipNodeSchedule]:
+        return list(self._nodes.values())
+
+    def node(self, name: str) -> HipNodeSchedule | None:
+        return self._nodes.get(name)
+
+    def __str__(self) -> str:
+        return str([str(s) for s in self._nodes.values()])

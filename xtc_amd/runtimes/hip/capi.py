@@ -230,3 +230,14 @@ def gemm_instances() -> list[dict[str, Any]]:
             }
         )
     return out
+
+
+_DTYPE_IDS = {"float32": XTC_HIP_F32, "bfloat16": XTC_HIP_BF16}
+
+
+def default_tile(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int], int]:
+    """(tile, split_k) the library picks for a shape when none is given."""
+    t = Tile()
+    sk = ctypes.c_int(1)
+    check(lib().xtc_hip_default_tile(_DTYPE_IDS[dtype], int(conv), M, N, K, ctypes.byref(t), ctypes.byref(sk)), "default_tile")
+    return t.as_tuple(), int(sk.value)

@@ -1,22 +1,42 @@
 # SPDX-License-Identifier: BSD-3-Clause
 """bfloat16 storage helpers for numpy (numpy has no native bf16).
 
-bf16 tensors are stored as uint16 bit patterns.  XTC graphs name the dtype
-"bfloat16"; the reference has no bf16 type (its numpy dtype map stops at
-float64, src/xtc/runtimes/types/ndarray.py:28-39), so this is an extension.
+Graphs name the dtype "bfloat16".  On the host such a tensor is a float32
+array whose values are bf16-representable; it becomes uint16 bit patterns
+only when copied to the device.  The reference has no bf16 type (its numpy
+dtype map stops at float64, src/xtc/runtimes/types/ndarray.py:28-39), so this
+is an extension.
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-__all__ = ["BF16", "f32_to_bf16_bits", "bf16_bits_to_f32", "round_to_bf16", "is_bf16"]
+__all__ = [
+    "BF16",
+    "f32_to_bf16_bits",
+    "bf16_bits_to_f32",
+    "round_to_bf16",
+    "is_bf16",
+    "host_dtype",
+    "itemsize",
+]
 
 BF16 = "bfloat16"
 
 
 def is_bf16(dtype: object) -> bool:
     return str(dtype) == BF16
+
+
+def host_dtype(dtype: object) -> np.dtype:
+    """numpy dtype used on the host for a graph dtype."""
+    return np.dtype(np.float32) if is_bf16(dtype) else np.dtype(str(dtype))
+
+
+def itemsize(dtype: object) -> int:
+    """Bytes per element on the device."""
+    return 2 if is_bf16(dtype) else np.dtype(str(dtype)).itemsize
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
