@@ -272,3 +272,64 @@ def test_memset_zero():
     B = DeviceBuffer.from_numpy(np.ones(1031, np.uint8))
     B.zero()
     assert not B.to_numpy((1031,), np.uint8).any()
+
+
+# ------------------------------------------- LDS-DMA bf16 kernel (256x256x64)
+
+
+def _run_strided(a, b, tile, lda, ldb, ldc, relu=False, bias=None):
+    """bf16 matmul with padded leading dimensions (elements)."""
+    M, K = a.shape
+    N = b.shape[1]
+    ap = np.zeros((M, lda), np.float32)
+    ap[:, :K] = a
+    bp = np.zeros((K, ldb), np.float32)
+    bp[:, :N] = b
+    A, B = _dev(ap, "bfloat16"), _dev(bp, "bfloat16")
+    C = DeviceBuffer(M * ldc * 4)
+    C.zero()
+    bias_buf = DeviceBuffer.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    d = capi.MatmulDesc()
+    d.dtype = capi.XTC_HIP_BF16
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = lda, ldb, ldc
+    d.tile = capi.Tile(*tile)
+    d.split_k = 1
+    d.xcd_remap = 1
+    d.relu = int(relu)
+    L = capi.lib()
+    capi.check(L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, bias_buf.c_ptr if bias_buf else None))
+    capi.check(L.xtc_hip_synchronize())
+    return C.to_numpy((M, ldc), np.float32)[:, :N]
+
+
+@pytest.mark.parametrize("waves", [(2, 4), (4, 2)])
+def test_lds_dma_bf16_integer_exact(waves):
+    M, N, K = 512, 768, 1024
+    a = ref.np_init((M, K), "float32")
+    b = (ref.np_init((K, N), "float32")[::-1]).copy()
+    out = run_matmul(a, b, "bfloat16", tile=(256, 256, 64, *waves))
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
+
+
+@pytest.mark.parametrize("waves", [(2, 4), (4, 2)])
+def test_lds_dma_bf16_seeded_bias_relu_strided(waves):
+    rng = np.random.default_rng(21)
+    M, N, K = 256, 512, 320
+    a = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    out = _run_strided(a, b, (256, 256, 64, *waves), lda=K + 64, ldb=N + 256, ldc=N + 4, relu=True, bias=bias)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_BF16
+
+
+def test_lds_dma_bf16_swizzle_covers_every_position():
+    # A and B hold distinct small integers at every (row, k) / (k, col), so any
+    # swizzle or transpose mistake changes the exact result
+    M, N, K = 256, 256, 64
+    a = ((np.arange(M)[:, None] * 3 + np.arange(K)[None, :] * 5) % 7 - 3).astype(np.float32)
+    b = ((np.arange(K)[:, None] * 11 + np.arange(N)[None, :] * 2) % 9 - 4).astype(np.float32)
+    for waves in ((2, 4), (4, 2)):
+        out = run_matmul(a, b, "bfloat16", tile=(256, 256, 64, *waves))
+        np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))

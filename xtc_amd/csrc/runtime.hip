@@ -12,6 +12,7 @@
 #include <mutex>
 #include <string>
 
+#include "gemm_bf16_lds.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
 
@@ -301,6 +302,8 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
     }
   }
   if (!f32 && M >= 4096 && N >= 4096) {
+    // aligned shapes take the LDS-DMA kernel behind this tile
+    if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && pick(256, 256, 64, 2, 4)) return;
     if (pick(256, 256, 64, 2, 2)) return;
   }
   if (M >= 2048 && N >= 2048) {
@@ -351,6 +354,56 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The LDS-DMA bf16 kernel (gemm_bf16_lds.hpp) implements the 256x256x64
+// tiles with 2x4 and 4x2 waves when the shape needs no bounds checks.
+// XTC_HIP_GENERIC_GEMM=1 forces the generic template (for A/B comparisons).
+bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
+                          int ldb, int ldc, const void* A, const void* B, const void* C,
+                          const void* bias) {
+  static const bool disabled = [] {
+    const char* v = getenv("XTC_HIP_GENERIC_GEMM");
+    return v && v[0] == '1';
+  }();
+  if (disabled || d.dtype != XTC_HIP_BF16 || split_k > 1) return false;
+  if (t.bm != 256 || t.bn != 256 || t.bk != 64) return false;
+  if (!((t.wgm == 2 && t.wgn == 4) || (t.wgm == 4 && t.wgn == 2))) return false;
+  if (d.M % 256 || d.N % 256 || d.K % 64) return false;
+  if (lda % 8 || ldb % 8 || ldc % 4) return false;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
+  // element offsets of one tile row/column range must fit in 32 bits
+  if ((int64_t)256 * lda > INT32_MAX || (int64_t)64 * ldb > INT32_MAX) return false;
+  return true;
+}
+
+int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int lda, int ldb,
+                        int ldc, const void* A, const void* B, float* C, const float* bias,
+                        hipStream_t s) {
+  BigGemmArgs a;
+  a.A = (const __bf16*)A;
+  a.B = (const __bf16*)B;
+  a.C = C;
+  a.bias = bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  a.tiles_m = d.M / 256;
+  a.tiles_n = d.N / 256;
+  a.group_m = d.group_m > 0 ? d.group_m : 8;
+  a.xcd_remap = d.xcd_remap;
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  if (t.wgm == 2)
+    hipLaunchKernelGGL((gemm_bf16_256x256x64<2, 4>), grid, dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_bf16_256x256x64<4, 2>), grid, dim3(512), 0, s, a);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
 
 }  // namespace
 
@@ -559,6 +612,8 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
   if (!e)
     return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
+    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = A;
