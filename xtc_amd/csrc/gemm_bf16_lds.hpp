@@ -1,30 +1,41 @@
 // SPDX-License-Identifier: BSD-3-Clause
 // bf16 GEMM for aligned large shapes on gfx950 (CDNA4):
 //   C[M,N] (fp32) = epilogue( A[M,K] (bf16, row-major) @ B[K,N] (bf16, row-major) )
-// with M % 256 == 0, N % 256 == 0, K % 64 == 0 and 16-byte aligned rows.
+// with M % 256 == 0, N % 256 == 0, K % BK == 0 and 16-byte aligned rows.
 //
-// Design (one 256x256 output tile per workgroup, 4 waves, one wave per SIMD):
-//   * K is walked in 64-deep slabs through two LDS stages of 64 KB each.
-//     Global -> LDS moves use the gfx950 LDS DMA (global_load_lds_dwordx4):
-//     no VGPR staging, no ds_write; slab k+1 streams in while slab k is
-//     multiplied; one s_waitcnt vmcnt(0) + barrier per slab.
-//   * A stays row-major in LDS (256 rows x 128 B).  Fragments are read with
-//     ds_read_b128; the 16-byte chunk of row r is XOR-swizzled by
-//     h(r) = (r & 7) ^ ((r >> 3) & 1), which makes the 16 rows a fragment read
-//     touches hit distinct banks for 32- and 64-bank LDS alike.
-//   * B stays row-major in LDS (64 k-rows x 512 B) and is read transposed by
+// Design (one 256x256 output tile per workgroup, WGM x WGN waves):
+//   * K is walked in BK-deep slabs through STAGES LDS stages (distinct LDS
+//     objects, so the compiler can tell the DMA into one stage from the reads
+//     of another).  Global -> LDS moves use the gfx950 LDS DMA
+//     (global_load_lds_dwordx4): no VGPR staging, no ds_write.  The DMA runs
+//     STAGES-1 slabs ahead of the MFMAs; per slab one s_waitcnt vmcnt(N) for
+//     exactly the slab about to be read, then one barrier.  Measured on
+//     MI355X at 8192^3: the DMA stream alone takes ~720-800 us (~11 TB/s
+//     from L2) against ~450 us of MFMA, so this kernel is bound by the L2
+//     delivery of the A/B panels; BK = 64 with 2 stages beat BK = 32 with 3-5
+//     stages (the per-slab barrier and first LDS reads cost more than the
+//     deeper prefetch gains).
+//   * A stays row-major in LDS (256 rows x 2*BK bytes), read with
+//     ds_read_b128.  The 16-byte chunk of row r is XOR-swizzled by r & 7 for
+//     128-byte rows (BK=64) and by (r >> 1) & 3 for 64-byte rows (BK=32): the
+//     best patterns measured for this access on MI355X (174 and 218 B/clk/CU;
+//     contiguous b128 reads give 191).
+//   * B stays row-major in LDS (BK k-rows x 512 B) and is read transposed by
 //     ds_read_b64_tr_b16: within a 16-lane group, output lane i element q is
 //     element (i % 4) of the 8 bytes addressed by lane 4q + i/4, so lane j
 //     addresses B[k0 + j/4][n0 + 4(j%4) .. +3] to receive B[k0 .. k0+3][n0+j].
 //     Two such reads give the 8 k-values of an MFMA operand.  The 32-byte chunk
-//     of k-row k is XOR-swizzled by (k & 3) | ((k >> 1) & 4) for the same
-//     bank-conflict reason.
-//   * Each wave owns a 128x128 sub-tile: 8x8 v_mfma_f32_16x16x32_bf16 tiles,
-//     256 fp32 accumulators per lane.  The MFMA operands are swapped
+//     of k-row k is XOR-swizzled by (k & 3) | ((k >> 1) & 4): 101 B/clk/CU
+//     measured (32 unswizzled, 94 with k & 3 alone).
+//   * Each wave owns a (256/WGM) x (256/WGN) sub-tile of
+//     v_mfma_f32_16x16x32_bf16 tiles.  The MFMA operands are swapped
 //     (B-fragment first) so each lane ends up holding 4 consecutive columns of
-//     one C row: the epilogue (bias, relu) stores float4s.
+//     one C row: the epilogue (bias, relu) stores float4s, row by row.
 //   * Workgroups are remapped so each XCD owns a contiguous range of tiles,
-//     rastered in groups of `group_m` tile rows for L2 reuse.
+//     rastered in groups of `group_m` tile rows for L2 reuse, and each tile
+//     starts its K walk at a tile-dependent slab (see kofs) so tiles sharing a
+//     panel are not in lockstep.  The rotation changes only the order of the
+//     fp32 accumulation.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -50,21 +61,22 @@ namespace big {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int NT = 256;                       // 4 waves
-constexpr int A_STAGE = BM * BK * 2;          // 32 KB
-constexpr int B_STAGE = BK * BN * 2;          // 32 KB
-constexpr int STAGE = A_STAGE + B_STAGE;      // 64 KB
+constexpr int BM = 256, BN = 256;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
-__device__ __forceinline__ int swz_a(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+template <int BK>
+__device__ __forceinline__ int swz_a(int row) {
+  return BK == 64 ? (row & 7) : ((row >> 1) & 3);
+}
 __device__ __forceinline__ int swz_b(int k) { return (k & 3) | ((k >> 1) & 4); }
+
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only.
+constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 
 __device__ __forceinline__ void tile_of_block(const BigGemmArgs& a, int& tm, int& tn) {
   const int nb = a.tiles_m * a.tiles_n;
@@ -79,10 +91,6 @@ __device__ __forceinline__ void tile_of_block(const BigGemmArgs& a, int& tm, int
   tn = in_group / gsize;
 }
 
-}  // namespace big
-
-namespace big {
-
 // Fragments of one 32-deep k-step for a wave's (16*TM) x (16*TN) sub-tile.
 template <int TM, int TN>
 struct Frags {
@@ -90,16 +98,15 @@ struct Frags {
   bf16x8 b[TN];
 };
 
-// Reads k-step `ks` of a stage (A at `sa`, B at `sa + A_STAGE`).
+// Reads k-step `ks` of a stage (A at `sa`, B at `sb`).
 //   A fragment `it`: lane (l16, g) gets A[row0 + it*16 + l16][ks*32 + 8g .. +7]
 //   B fragment `jt`: lane (l16, g) gets B[ks*32 + 8g .. +7][col0 + jt*16 + l16]
-template <int TM, int TN>
-__device__ __forceinline__ void read_frags(Frags<TM, TN>& f, const unsigned char* sa, int ks, int a_row0, int a_h,
-                                           int g, int b_krow0, int b_f, int b_c0, int l16) {
-  const unsigned char* sb = sa + A_STAGE;
+template <int BK, int TM, int TN>
+__device__ __forceinline__ void read_frags(Frags<TM, TN>& f, const unsigned char* sa, const unsigned char* sb, int ks,
+                                           int a_row0, int a_h, int g, int b_krow0, int b_f, int b_c0, int l16) {
 #pragma unroll
   for (int it = 0; it < TM; ++it) {
-    const int off = (a_row0 + it * 16) * 128 + 16 * ((ks * 4 + g) ^ a_h);
+    const int off = (a_row0 + it * 16) * (2 * BK) + 16 * ((ks * 4 + g) ^ a_h);
     f.a[it] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sa + off));
   }
 #pragma unroll
@@ -124,19 +131,31 @@ __device__ __forceinline__ void mma(f32x4 (&acc)[TM][TN], const Frags<TM, TN>& f
 }  // namespace big
 
 // WGM x WGN waves; each wave owns a (256/WGM) x (256/WGN) sub-tile.
-template <int WGM, int WGN>
+template <int WGM, int WGN, int BK, int STAGES>
 __global__ void __attribute__((amdgpu_flat_work_group_size(WGM * WGN * 64, WGM * WGN * 64)))
-gemm_bf16_256x256x64(BigGemmArgs args) {
+gemm_bf16_256x256(BigGemmArgs args) {
   using namespace big;
   constexpr int WAVES = WGM * WGN;
   constexpr int TM = BM / WGM / 16;
   constexpr int TN = BN / WGN / 16;
+  constexpr int A_STAGE = BM * BK * 2;
+  constexpr int B_STAGE = BK * BN * 2;
+  constexpr int STAGE = A_STAGE + B_STAGE;
   constexpr int KB_PER_WAVE = (A_STAGE / 1024) / WAVES;  // DMA kilobytes per operand per wave
+  constexpr int DMA_PER_SLAB = 2 * KB_PER_WAVE;           // DMA instructions per wave per slab
+  constexpr int A_ROWS_PER_KB = 1024 / (2 * BK);
+  constexpr int A_CHUNKS = (2 * BK) / 16;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(STAGES >= 2 && STAGES <= 5 && STAGES * STAGE <= 160 * 1024, "LDS");
   static_assert(KB_PER_WAVE * WAVES * 1024 == A_STAGE, "stage must split evenly over waves");
-  // Two distinct LDS objects, one per stage, so the compiler can tell the
-  // DMA into one stage from the fragment reads of the other.
-  __shared__ __attribute__((aligned(1024))) unsigned char stage0[STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char stage1[STAGE];
+  static_assert((STAGES - 2) * DMA_PER_SLAB < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char st2[STAGES > 2 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char st3[STAGES > 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char st4[STAGES > 4 ? STAGE : 16];
+  unsigned char* const stages[5] = {st0, st1, st2, st3, st4};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -156,8 +175,8 @@ gemm_bf16_256x256x64(BigGemmArgs args) {
 #pragma unroll
   for (int i = 0; i < KB_PER_WAVE; ++i) {
     const int kb = wave * KB_PER_WAVE + i;
-    const int arow = kb * 8 + (lane >> 3);  // A: 8 rows of 128 B per KB
-    a_off[i] = arow * args.lda + ((lane & 7) ^ swz_a(arow)) * 8;
+    const int arow = kb * A_ROWS_PER_KB + lane / A_CHUNKS;
+    a_off[i] = arow * args.lda + ((lane % A_CHUNKS) ^ swz_a<BK>(arow)) * 8;
     const int bk = kb * 2 + (lane >> 5);  // B: 2 k-rows of 512 B per KB
     const int slot = lane & 31;
     b_off[i] = bk * args.ldb + ((slot >> 1) ^ swz_b(bk)) * 16 + (slot & 1) * 8;
@@ -165,10 +184,20 @@ gemm_bf16_256x256x64(BigGemmArgs args) {
   const __bf16* a_base = args.A + (size_t)m0 * args.lda;
   const __bf16* b_base = args.B + n0;
   const size_t b_step = (size_t)BK * args.ldb;
+  const int nk = args.K / BK;
+  // K-stagger: tile (tm, tn) walks K starting at slab (tm + 2 tn) mod 16, so
+  // the tiles sharing an A panel (same tm) or a B panel (same tn) do not
+  // request the same lines at the same time: one leads and takes the L2
+  // miss, the others trail and hit.  In lockstep, nearly every L2 access
+  // waited on a miss in flight (measured: 830 -> 787 us at 8192^3).
+  int kofs = (tile_m + 2 * tile_n) & 15;
+  kofs = nk > 0 ? kofs % nk : 0;
 
   auto issue_slab = [&](int kt, unsigned char* st) {
-    const __bf16* ab = a_base + (size_t)kt * BK;
-    const __bf16* bb = b_base + (size_t)kt * b_step;
+    int kr = kt + kofs;
+    kr = kr >= nk ? kr - nk : kr;
+    const __bf16* ab = a_base + (size_t)kr * BK;
+    const __bf16* bb = b_base + (size_t)kr * b_step;
 #pragma unroll
     for (int i = 0; i < KB_PER_WAVE; ++i)
       __builtin_amdgcn_global_load_lds((const void*)(ab + a_off[i]),
@@ -183,7 +212,7 @@ gemm_bf16_256x256x64(BigGemmArgs args) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int a_row0 = wm * (16 * TM) + l16;
-  const int a_h = swz_a(a_row0);        // depends on l16 only
+  const int a_h = swz_a<BK>(a_row0);    // depends on l16 only
   const int b_krow0 = 8 * g + (l16 >> 2);
   const int b_f = swz_b(b_krow0);       // unchanged by ks*32 and the +4 half
   const int b_c0 = wn * TN;             // first 32-byte chunk of the wave's columns
@@ -194,43 +223,49 @@ gemm_bf16_256x256x64(BigGemmArgs args) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = args.K / BK;
-  auto slab = [&](int kt, unsigned char* cur, unsigned char* nxt) {
-    if (kt + 1 < nk) issue_slab(kt + 1, nxt);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) issue_slab(s, stages[s]);
+
+  // slab kt lives in stage kt % STAGES; the unrolled body fixes it at compile time
+  auto step = [&](int kt, const int s) {
+    if (kt + STAGES - 2 < nk)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * DMA_PER_SLAB));  // slab kt landed
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();  // slab kt visible to all waves; stage of slab kt-1 free
+    if (kt + STAGES - 1 < nk) issue_slab(kt + STAGES - 1, stages[(s + STAGES - 1) % STAGES]);
+    const unsigned char* sa = stages[s];
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
       Frags<TM, TN> f;
-      read_frags(f, cur, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
+      read_frags<BK>(f, sa, sa + A_STAGE, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
       mma(acc, f);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // DMA of slab kt+1 landed
-    __syncthreads();                // every wave is done with `cur`
   };
-
-  issue_slab(0, stage0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    slab(kt, stage0, stage1);
-    if (kt + 1 < nk) slab(kt + 1, stage1, stage0);
+  for (int kt = 0; kt < nk; kt += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+      if (kt + s < nk) step(kt + s, s);
   }
 
-  // ---- epilogue: lane holds C[m][n .. n+3] for each (it, jt)
+  // ---- epilogue: lane holds C[m][n .. n+3] for each (it, jt); rows in order
   const int mrow = m0 + wm * (16 * TM) + l16;
   const int ncol = n0 + wn * (16 * TN) + 4 * g;
+  f32x4 bv[TN];
 #pragma unroll
-  for (int jt = 0; jt < TN; ++jt) {
-    const int n = ncol + jt * 16;
-    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-    if (args.bias) bv = *(const f32x4*)(args.bias + n);
+  for (int jt = 0; jt < TN; ++jt)
+    bv[jt] = args.bias ? *(const f32x4*)(args.bias + ncol + jt * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int it = 0; it < TM; ++it) {
-      f32x4 v = acc[it][jt] + bv;
+  for (int it = 0; it < TM; ++it) {
+#pragma unroll
+    for (int jt = 0; jt < TN; ++jt) {
+      f32x4 v = acc[it][jt] + bv[jt];
       if (args.relu) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = v[r] < args.relu_threshold ? args.relu_threshold : v[r];
       }
-      *(f32x4*)(args.C + (size_t)(mrow + it * 16) * args.ldc + n) = v;
+      *(f32x4*)(args.C + (size_t)(mrow + it * 16) * args.ldc + ncol + jt * 16) = v;
     }
   }
 }
