@@ -1,0 +1,129 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""`loop-explore` for the HIP backend (src/xtc/cli/explore.py:52-355).
+
+  python -m xtc_amd.cli.explore --operator matmul --dims 4096 4096 4096 \
+      --dtype float32 --backends hip --strategy tile_pprprp --search random \
+      --trials 64 --seed 0 --output c2.csv
+
+Flags follow the reference where they apply (operator, dims, dtype,
+strategy, search, backends, trials, seed, threads, max-unroll, opt-level,
+output, db-file, resume, append, graph-file, peak-flops, data).  The
+reference re-executes itself under `setarch -R` to disable ASLR for CPU
+timing stability; GPU timing does not need it, so this driver runs in-process.
+"""
+
+from __future__ import annotations
+
+import argparse
+import logging
+import os
+import sys
+from typing import Any
+
+from ..search.explore import Exploration, ExplorationConfig
+from ..search.strategies import Strategies
+
+DEFAULT_DIMS = {"matmul": [512, 512, 512], "conv2d": [8, 56, 56, 64, 3, 3, 64, 1, 1]}
+
+
+def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0) -> Any:
+    """Graphs of the reference's `--operator` choices (explore.py:151-260)."""
+    import xtc_amd.graphs.xtc.op as O
+
+    extra = {"out_dtype": "float32"} if dtype == "bfloat16" else {}
+    if operator == "matmul":
+        i, j, k = dims
+        a = O.tensor((i, k), dtype, name="A")
+        b = O.tensor((k, j), dtype, name="B")
+        with O.graph(name="matmul") as gb:
+            O.matmul(a, b, name="C", **extra)
+        return gb.graph
+    if operator == "conv2d":
+        n, h, w, f, r, s, c, sh, sw = (dims + [1, 1])[:9]
+        ih, iw = (h - 1) * sh + r - 2 * pad, (w - 1) * sw + s - 2 * pad
+        x = O.tensor((n, ih, iw, c), dtype, name="I")
+        wt = O.tensor((r, s, c, f), dtype, name="W")
+        with O.graph(name="conv2d") as gb:
+            src = O.pad2d(x, padding=pad, axes=(1, 2)) if pad else x
+            O.conv2d(src, wt, name="conv", stride=(sh, sw), **extra)
+        return gb.graph
+    raise SystemExit(f"unknown operator {operator}")
+
+
+def main(argv: list[str] | None = None) -> int:
+    p = argparse.ArgumentParser(prog="loop-explore", description=__doc__.split("\n\n")[0])
+    p.add_argument("--operator", default="matmul", choices=["matmul", "conv2d"])
+    p.add_argument("--graph-file", help="YAML graph (Graph.dump format) instead of --operator")
+    p.add_argument("--dims", nargs="+", type=int, help="operator dimensions")
+    p.add_argument("--pad", type=int, default=0, help="conv2d: pad2d producer on H and W")
+    p.add_argument("--dtype", default="float32", choices=["float32", "bfloat16"])
+    p.add_argument("--strategy", default="tile_hip", help=f"one of {Strategies.names(include_aliases=True)}")
+    p.add_argument("--search", default="random", choices=["random", "exhaustive", "data", "default"])
+    p.add_argument("--data", help="CSV of samples for --search data")
+    p.add_argument("--backends", nargs="+", default=["hip"], choices=["hip"])
+    p.add_argument("--trials", type=int, default=64)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--threads", type=int, default=1, help="strategy threads (parallel outer axes)")
+    p.add_argument("--max-unroll", type=int, default=256)
+    p.add_argument("--vec-size", type=int, default=16)
+    p.add_argument("--opt-level", type=int, default=2)
+    p.add_argument("--repeat", type=int, default=5)
+    p.add_argument("--number", type=int, default=1)
+    p.add_argument("--min-repeat-ms", type=int, default=100)
+    p.add_argument("--validate", action="store_true")
+    p.add_argument("--pmu-counters", nargs="*", default=[])
+    p.add_argument("--jobs", type=int, default=max(1, min(16, (os.cpu_count() or 2) // 2)))
+    p.add_argument("--output", default="results.csv")
+    p.add_argument("--db-file")
+    p.add_argument("--resume", action="store_true")
+    p.add_argument("--append", action="store_true")
+    p.add_argument("--peak-flops", type=float, help="peak FMA/s (default: device MFMA peak)")
+    p.add_argument("--debug", action="store_true")
+    args = p.parse_args(argv)
+    logging.basicConfig(level=logging.DEBUG if args.debug else logging.INFO, format="%(message)s")
+
+    if args.graph_file:
+        import xtc_amd.graphs.xtc.op as O
+
+        with O.graph() as gb:
+            O.graph.load(args.graph_file)
+        graph = gb.graph
+    else:
+        graph = build_graph(args.operator, args.dims or DEFAULT_DIMS[args.operator], args.dtype, args.pad)
+    strat_kwargs = {"threads": args.threads, "max_unroll": args.max_unroll, "vec_size": args.vec_size}
+    if Strategies.resolve_name(args.strategy) == "tile_hip":
+        strat_kwargs = {}
+    for backend in args.backends:
+        cfg = ExplorationConfig(
+            backend=backend,
+            strategy=args.strategy,
+            strategy_kwargs=strat_kwargs,
+            search=args.search,
+            trials=args.trials,
+            seed=args.seed,
+            opt_level=args.opt_level,
+            data=args.data,
+            repeat=args.repeat,
+            number=args.number,
+            min_repeat_ms=args.min_repeat_ms,
+            validate=args.validate,
+            pmu_counters=args.pmu_counters,
+            jobs=args.jobs,
+            output=args.output,
+            db_file=args.db_file,
+            resume=args.resume,
+            append=args.append,
+            peak_flops=args.peak_flops,
+        )
+        results = Exploration(graph, cfg).run()
+        ok = [(min(t), s) for s, t, code, _ in results if code == 0 and t]
+        if ok:
+            best_t, best_s = min(ok)
+            print(f"{backend}: best {best_s} {best_t * 1e6:.1f} us over {len(ok)}/{len(results)} samples", flush=True)
+        else:
+            print(f"{backend}: no successful sample ({len(results)} tried)", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

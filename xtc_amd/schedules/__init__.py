@@ -1,0 +1,1 @@
+# SPDX-License-Identifier: BSD-3-Clause

@@ -1,0 +1,257 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""Schedule exploration driver (the engine of `loop-explore`,
+src/xtc/search/explore.py:200-873, src/xtc/search/pipeline.py:28-117,
+src/xtc/search/callback.py:22-172).
+
+Per sample: Backend(graph) -> get_scheduler() -> strategy.generate(sch, x)
+-> schedule() -> get_compiler(...).compile() -> module.get_evaluator(...)
+.evaluate(); time = min over repeats.  Compilation runs on a thread pool
+(`jobs`), execution on one thread, as in the reference pipeline.  Results go
+to a CSV with the reference's layout (sample columns, X, time, peak,
+backend), optionally to a JSON-lines DB, and a `<output>.meta.json` run
+manifest records the arguments.  Failed samples get time 0 and are logged,
+and are not written to the CSV (callback.py:152-154).
+
+With the HIP backend the strategy's samples are filtered to those that map
+exactly onto a compiled kernel instance (schedule_policy "strict"), so every
+measured point is the schedule it claims to be.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import csv
+import json
+import logging
+import os
+import platform
+import subprocess
+import sys
+import time
+from dataclasses import asdict, dataclass, field
+from datetime import datetime, timezone
+from importlib import import_module
+from pathlib import Path
+from typing import Any, Callable
+
+from .strategies import Strategies
+
+__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter"]
+
+logger = logging.getLogger("xtc_amd.search")
+
+
+@dataclass
+class ExplorationConfig:
+    backend: str = "hip"
+    strategy: str = "tile_hip"
+    strategy_kwargs: dict[str, Any] = field(default_factory=dict)
+    search: str = "random"  # "random" | "exhaustive" | "data"
+    trials: int = 64
+    seed: int = 0
+    opt_level: int = 2
+    data: str | None = None  # CSV of samples for search "data"
+    repeat: int = 5
+    number: int = 1
+    min_repeat_ms: int = 100
+    validate: bool = False
+    pmu_counters: list[str] = field(default_factory=list)
+    jobs: int = max(1, (os.cpu_count() or 2) // 2)
+    output: str = "results.csv"
+    db_file: str | None = None
+    resume: bool = False
+    append: bool = False
+    peak_flops: float | None = None  # FMA/s; default: the device's dense MFMA peak
+    compile_kwargs: dict[str, Any] = field(default_factory=dict)
+
+
+class CSVCallback:
+    """Writes one row per successful sample; `resume` skips (backend, sample)
+    pairs already in the file, `append` appends without a new header."""
+
+    def __init__(self, fname: str, peak_time: float, sample_names: list[str], *, resume: bool = False,
+                 append: bool = False) -> None:
+        self._fname = fname
+        self._peak_time = peak_time
+        self._names = sample_names
+        self.seen: set[tuple[str, tuple[int, ...]]] = set()
+        path = Path(fname)
+        existing = path.exists() and path.stat().st_size > 0
+        if resume and existing:
+            with open(path, newline="") as f:
+                for row in csv.DictReader(f):
+                    try:
+                        self.seen.add((row["backend"], tuple(int(row[n]) for n in self._names)))
+                    except (KeyError, TypeError, ValueError):
+                        continue
+        mode = "a" if (resume or append) else "w"
+        self._f = open(path, mode, newline="")
+        self._w = csv.writer(self._f)
+        if mode == "w" or not existing:
+            self._w.writerow(self._names + ["X", "time", "peak", "backend"])
+            self._f.flush()
+
+    def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str) -> None:
+        if code != 0 or not times:
+            return
+        t = min(times)
+        self._w.writerow([*sample, str(list(sample)), t, self._peak_time / t if t > 0 else 0.0, backend])
+        self._f.flush()
+        self.seen.add((backend, tuple(sample)))
+
+    def close(self) -> None:
+        self._f.close()
+
+
+class DBCallback:
+    """JSON-lines record per sample (successes and failures)."""
+
+    def __init__(self, fname: str, graph_name: str, strategy: str) -> None:
+        self._f = open(fname, "a")
+        self._graph = graph_name
+        self._strategy = strategy
+
+    def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str,
+                 extra: dict[str, Any] | None = None) -> None:
+        rec = {"graph": self._graph, "strategy": self._strategy, "backend": backend, "sample": list(sample),
+               "results": times, "code": code, "error": msg, **(extra or {})}
+        self._f.write(json.dumps(rec) + "\n")
+        self._f.flush()
+
+    def close(self) -> None:
+        self._f.close()
+
+
+def hip_sample_filter(graph: Any, strategy_factory: Callable[..., Any]) -> Callable[[list[int]], bool]:
+    """Predicate: does this sample's schedule map exactly onto a compiled
+    kernel instance?  Builds the schedule on a scratch HipBackend."""
+    from ..backends.hip import Backend
+    from ..backends.hip.mapping import map_gemm
+    from ..backends.hip.scheduler import ScheduleError
+
+    backend = Backend(graph)
+    probe = strategy_factory()
+    cache: dict[tuple[int, ...], bool] = {}
+
+    def ok(sample: list[int]) -> bool:
+        key = tuple(sample)
+        if key not in cache:
+            sch = backend.get_scheduler()
+            try:
+                probe.generate(sch, list(sample))
+                schedule = sch.schedule()
+                for ln in backend.plan.launches:
+                    if ln.kind in ("matmul", "conv2d"):
+                        map_gemm(ln.attrs, ln.kind == "conv2d", schedule.node(ln.node), "strict")
+                cache[key] = True
+            except (ScheduleError, ValueError):
+                cache[key] = False
+        return cache[key]
+
+    return ok
+
+
+class Exploration:
+    def __init__(self, graph: Any, config: ExplorationConfig) -> None:
+        self.graph = graph
+        self.config = config
+        self._backend_mod = import_module(f"xtc_amd.backends.{config.backend}")
+        kwargs = dict(config.strategy_kwargs)
+        if config.backend == "hip" and Strategies.resolve_name(config.strategy) != "tile_hip":
+            kwargs["sample_filter"] = hip_sample_filter(
+                graph, lambda: Strategies.create(config.strategy, graph, **config.strategy_kwargs)
+            )
+        self.strategy = Strategies.create(config.strategy, graph, **kwargs)
+
+    # ---- sample sources
+    def samples(self) -> list[list[int]]:
+        c = self.config
+        if c.search == "exhaustive":
+            from itertools import islice
+
+            return [list(x) for x in islice(self.strategy.exhaustive(), c.trials)]
+        if c.search == "random":
+            return [list(x) for x in self.strategy.sample(c.trials, seed=c.seed)]
+        if c.search == "data":
+            if not c.data:
+                raise ValueError("search 'data' needs a data CSV")
+            with open(c.data, newline="") as f:
+                return [json.loads(row["X"]) for row in csv.DictReader(f)]
+        if c.search == "default":
+            return [list(self.strategy.default_schedule(c.opt_level))]
+        raise ValueError(f"unknown search {c.search!r}")
+
+    # ---- one sample
+    def compile_one(self, sample: list[int]) -> Any:
+        backend = self._backend_mod.Backend(self.graph)
+        sch = backend.get_scheduler()
+        self.strategy.generate(sch, sample)
+        kwargs = {"shared_lib": True, **self.config.compile_kwargs}
+        if self.config.backend == "hip":
+            kwargs.setdefault("schedule_policy", "strict")
+        return backend.get_compiler(**kwargs).compile(sch.schedule())
+
+    def evaluate_one(self, module: Any) -> tuple[list[float], int, str]:
+        c = self.config
+        return module.get_evaluator(
+            repeat=c.repeat, number=c.number, min_repeat_ms=c.min_repeat_ms, validate=c.validate,
+            pmu_counters=c.pmu_counters,
+        ).evaluate()
+
+    def peak_time(self) -> float:
+        peak = self.config.peak_flops
+        if peak is None and self.config.backend == "hip":
+            from ..runtimes.hip.device import HipDevice
+
+            peak = HipDevice().evaluate_flops(self.graph.ops_dtype())
+        return self.graph.ops_count() / peak if peak else 0.0
+
+    def write_manifest(self) -> None:
+        try:
+            commit = subprocess.run(["git", "rev-parse", "HEAD"], capture_output=True, text=True, check=True).stdout.strip()
+        except (OSError, subprocess.CalledProcessError):
+            commit = None
+        meta = {
+            "generatedAt": datetime.now(timezone.utc).isoformat(),
+            "output": self.config.output,
+            "sampleNames": self.strategy.sample_names,
+            "gitCommit": commit,
+            "python": {"version": sys.version, "executable": sys.executable},
+            "platform": {"platform": sys.platform, "machine": platform.machine(), "cwd": os.getcwd()},
+            "args": {k: (v if isinstance(v, (str, int, float, bool, list, dict, type(None))) else str(v))
+                     for k, v in asdict(self.config).items()},
+        }
+        Path(f"{self.config.output}.meta.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
+
+    def run(self) -> list[tuple[list[int], list[float], int, str]]:
+        c = self.config
+        samples = self.samples()
+        csv_cb = CSVCallback(c.output, self.peak_time(), self.strategy.sample_names, resume=c.resume, append=c.append)
+        db_cb = DBCallback(c.db_file, self.graph.name, c.strategy) if c.db_file else None
+        self.write_manifest()
+        todo = [s for s in samples if (c.backend, tuple(s)) not in csv_cb.seen]
+        results: list[tuple[list[int], list[float], int, str]] = []
+        t0 = time.time()
+        with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
+            futures = [pool.submit(self.compile_one, s) for s in todo]
+            for idx, (sample, fut) in enumerate(zip(todo, futures)):
+                extra: dict[str, Any] = {}
+                try:
+                    module = fut.result()
+                    extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()}}
+                    times, code, msg = self.evaluate_one(module)
+                except Exception as err:  # a failed sample is recorded, not fatal
+                    times, code, msg = [], 2, f"{type(err).__name__}: {err}"
+                if code:
+                    logger.warning("sample %s failed: %s", sample, msg)
+                results.append((sample, times, code, msg))
+                csv_cb(sample, c.backend, times, code, msg)
+                if db_cb:
+                    db_cb(sample, c.backend, times, code, msg, extra)
+                best = min(times) if times else 0.0
+                logger.info("[%d/%d] %s -> %.3g s (%s)", idx + 1, len(todo), sample, best, msg or "ok")
+        csv_cb.close()
+        if db_cb:
+            db_cb.close()
+        logger.info("explored %d samples in %.1f s", len(todo), time.time() - t0)
+        return results
