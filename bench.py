@@ -141,6 +141,31 @@ def _traffic(cfg: str) -> float | None:
     return None
 
 
+def _vendor_matmul(host_in: list[np.ndarray], dtype: str, steps: int, warmup: int) -> dict:
+    """Times torch.matmul (hipBLASLt on this image) on the same inputs as a
+    reference point for the vendor library; bf16 inputs give a bf16 output
+    there (half the output bytes of the fp32 output measured here)."""
+    import torch
+
+    tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float32
+    a = torch.from_numpy(host_in[0]).to("cuda:0").to(tdt).contiguous()
+    b = torch.from_numpy(host_in[1]).to("cuda:0").to(tdt).contiguous()
+    for _ in range(warmup):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    m, k = host_in[0].shape
+    n = host_in[1].shape[1]
+    return {"library": "torch.matmul (hipBLASLt)", "out_dtype": str(tdt).split(".")[1], "kernel_ms": round(ms, 4),
+            "tflops": round(2 * m * n * k / ms / 1e9, 1)}
+
+
 def _cpu_baseline(cfg: str) -> dict:
     """Times the CPU restatement on a bounded sample of the workload."""
     from oracle import cpu_baseline as cb
@@ -170,6 +195,36 @@ def _cpu_baseline(cfg: str) -> dict:
     }
 
 
+COPY_BYTES = 1 << 30
+
+
+def _calibrate_copy(steps: int) -> int:
+    """Streams COPY_BYTES through the library's elementwise kernel
+    (relu_kernel, y = max(x, 0) over 2^28 fp32: exactly COPY_BYTES read and
+    COPY_BYTES written per launch).  Under rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE its per-dispatch KiB give the factor that turns those counters
+    into bytes for the GEMM dispatches."""
+    from xtc_amd.runtimes.hip import capi
+    from xtc_amd.runtimes.hip.device import HipDevice
+    from xtc_amd.runtimes.hip.ndarray import DeviceArray
+
+    dev = HipDevice(0)
+    dev.init_device()
+    n = COPY_BYTES // 4
+    x = DeviceArray((n,), "float32", dev)
+    y = DeviceArray((n,), "float32", dev)
+    x.fill_zero()
+    L = capi.lib()
+    for _ in range(steps):
+        capi.check(L.xtc_hip_relu(ctypes.c_void_p(x.data), ctypes.c_void_p(y.data), n, 0.0, None), "relu")
+    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    print(json.dumps({"calibration": "relu_kernel copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                      "launches": steps}), flush=True)
+    x.free()
+    y.free()
+    return 0
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -177,7 +232,13 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C3a", choices=["C1", "C2", "C3a", "C3b", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--vs-hipblaslt", action="store_true",
+                    help="also time torch.matmul on the same inputs (matmul configs) and report it in config")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="launch only the 1 GiB copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args(argv)
+    if args.calibrate_copy:
+        return _calibrate_copy(args.steps)
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: every box of this pool has one GPU; "
@@ -286,6 +347,8 @@ def main(argv: list[str] | None = None) -> int:
         },
         "roofline": roof,
     }
+    if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
+        line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup)
     if not args.no_cpu:
         try:
             line["cpu_baseline"] = _cpu_baseline(cfg)

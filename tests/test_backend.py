@@ -1,0 +1,326 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""HIP backend host logic on the CPU: lowering (fusions, workspace), the
+scheduler surface, schedule -> kernel mapping, payload code generation and
+the C-ABI library's exports.  Nothing here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import threading
+from pathlib import Path
+
+import pytest
+
+import xtc_amd.graphs.xtc.op as O
+from xtc_amd.backends.hip import Backend
+from xtc_amd.backends.hip.compiler import generate_payload
+from xtc_amd.backends.hip.lowering import UnsupportedGraph
+from xtc_amd.backends.hip.mapping import legal_tiles, map_gemm
+from xtc_amd.backends.hip.scheduler import ScheduleError
+from xtc_amd.runtimes.hip import capi
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _matmul(m, n, k, dtype="float32", name="mm", **kw):
+    a = O.tensor((m, k), dtype, name="A")
+    b = O.tensor((k, n), dtype, name="B")
+    with O.graph(name=name) as gb:
+        O.matmul(a, b, name="C", **kw)
+    return gb.graph
+
+
+def _conv_relu():
+    x = O.tensor((8, 56, 56, 64), "float32", name="I")
+    w = O.tensor((3, 3, 64, 64), "float32", name="W")
+    with O.graph(name="conv_relu") as gb:
+        p = O.pad2d(x, padding=1, axes=(1, 2), name="pad")
+        c = O.conv2d(p, w, name="conv")
+        O.relu(c, name="relu")
+    return gb.graph
+
+
+def _mlp():
+    x = O.tensor((2048, 1024), "float32", name="X")
+    w1 = O.tensor((1024, 4096), "float32", name="W1")
+    w2 = O.tensor((4096, 1024), "float32", name="W2")
+    with O.graph(name="mlp") as gb:
+        h = O.relu(O.matmul(x, w1, name="fc1"), name="act")
+        O.matmul(h, w2, name="fc2")
+    return gb.graph
+
+
+# ---------------------------------------------------------------- lowering
+
+def test_conv_pad_relu_fuse_into_one_launch():
+    plan = Backend(_conv_relu()).plan
+    (ln,) = plan.launches
+    assert ln.kind == "conv2d" and ln.node == "conv"
+    assert ln.absorbed == ["pad", "relu"]
+    assert ln.attrs["pads"] == (1, 1, 1, 1) and ln.attrs["relu"]
+    assert (ln.attrs["M"], ln.attrs["N"], ln.attrs["K"]) == (8 * 56 * 56, 64, 576)
+    assert (ln.attrs["H"], ln.attrs["W"]) == (56, 56)  # the loader reads the unpadded input
+    assert plan.workspace_bytes == 0
+
+
+def test_mlp_relu_epilogue_and_workspace():
+    plan = Backend(_mlp()).plan
+    assert [(l.kind, l.node, l.absorbed) for l in plan.launches] == [("matmul", "fc1", ["act"]), ("matmul", "fc2", [])]
+    temps = [b for b in plan.buffers.values() if b.kind == "temp"]
+    assert len(temps) == 1 and temps[0].nbytes == 2048 * 4096 * 4 and temps[0].offset % 256 == 0
+    assert plan.workspace_bytes == 2048 * 4096 * 4
+
+
+def test_relu_not_fused_when_intermediate_is_an_output():
+    a = O.tensor((64, 64), "float32")
+    b = O.tensor((64, 64), "float32")
+    with O.graph(name="fused") as gb:
+        O.relu(O.matmul(a, b, name="mm"), name="r")
+    # single consumer, not an output: fused
+    assert [l.kind for l in Backend(gb.graph).plan.launches] == ["matmul"]
+    with O.graph(name="two_outs") as gb:
+        c = O.matmul(a, b, name="mm")
+        r = O.relu(c, name="r")
+        O.outputs(c, r)
+    plan = Backend(gb.graph).plan
+    assert len(gb.graph.outputs) == 2
+    assert [l.kind for l in plan.launches] == ["matmul", "relu"]
+    assert not plan.launches[0].attrs["relu"]
+
+
+def test_unfused_pad_and_standalone_relu():
+    x = O.tensor((2, 5, 5, 3), "float32")
+    with O.graph(name="pad_relu") as gb:
+        O.relu(O.pad2d(x, padding=(1, 2), axes=(1, 2), constant_value=-1.0), threshold=0.5)
+    plan = Backend(gb.graph).plan
+    assert [l.kind for l in plan.launches] == ["pad", "relu"]
+    pad = plan.launches[0]
+    assert pad.attrs["pads"] == [(0, 0), (1, 2), (1, 2), (0, 0)] and pad.attrs["value"] == -1.0
+    assert plan.launches[1].attrs == {"threshold": 0.5, "n": 2 * 8 * 8 * 3}
+
+
+def test_bias_add_fuses_before_relu():
+    a = O.tensor((128, 64), "float32")
+    w = O.tensor((64, 32), "float32")
+    bias = O.tensor((32,), "float32")
+    with O.graph(name="fc") as gb:
+        O.relu(O.bias_add(O.matmul(a, w, name="mm"), bias))
+    (ln,) = Backend(gb.graph).plan.launches
+    assert ln.attrs["bias"] is not None and ln.attrs["relu"] and len(ln.absorbed) == 2
+
+
+def test_bf16_output_gets_a_cast_launch():
+    plan = Backend(_matmul(256, 256, 64, "bfloat16")).plan
+    assert [l.kind for l in plan.launches] == ["matmul", "cast"]
+    plan32 = Backend(_matmul(256, 256, 64, "bfloat16", out_dtype="float32")).plan
+    assert [l.kind for l in plan32.launches] == ["matmul"]
+
+
+def test_reshape_is_an_alias():
+    img = O.tensor((32, 32, 3), "float32")
+    w = O.tensor((3072, 16), "float32")
+    with O.graph(name="fc") as gb:
+        O.matmul(O.reshape(img, shape=(1, -1)), w)
+    plan = Backend(gb.graph).plan
+    assert [l.kind for l in plan.launches] == ["matmul"]
+    aliases = [b for b in plan.buffers.values() if b.kind == "alias"]
+    assert len(aliases) == 1 and plan.buffer(aliases[0].uid).kind == "input"
+
+
+def test_unsupported_operator_and_dtype_raise():
+    k = O.tensor((8, 5, 5, 3), "float32")
+    with O.graph(name="tr") as gb:
+        O.transpose(k, axes=(1, 2, 3, 0))
+    with pytest.raises(UnsupportedGraph):
+        Backend(gb.graph)
+    with pytest.raises(UnsupportedGraph):
+        Backend(_matmul(16, 16, 16, "float64"))
+
+
+# ---------------------------------------------------------------- scheduler
+
+def test_default_node_writes_the_output():
+    assert Backend(_conv_relu()).get_scheduler().node_name == "conv"
+    assert Backend(_mlp()).get_scheduler().node_name == "fc2"
+    assert Backend(_mlp()).get_scheduler(default_node="fc1").node_name == "fc1"
+    with pytest.raises(ScheduleError):
+        Backend(_mlp()).get_scheduler(default_node="nope")
+
+
+def test_schedule_records_primitives():
+    sch = Backend(_matmul(512, 512, 512)).get_scheduler()
+    sch.tile("i", {"i1": 128, "i2": 32})
+    sch.tile("j", {"j1": 128})
+    sch.interchange(["i", "j", "k", "i1", "j1", "i2"])
+    sch.parallelize(["i"])
+    sch.vectorize(["i2"])
+    sch.unroll({"i2": 4})
+    (s,) = sch.schedule().schedule_impl
+    assert s.tiles == {"i": {"i1": 128, "i2": 32}, "j": {"j1": 128}, "k": {}}
+    assert s.permutation["."][:3] == ["./i", "./j", "./k"]
+    assert s.parallelization == ["./i"] and s.vectorization == ["./i2"] and s.unrolling == {"./i2": 4}
+    assert "i1" in str(sch.schedule())
+    with pytest.raises(ScheduleError):
+        sch.tile("q", {"q1": 2})
+
+
+def test_meshes_are_rejected():
+    sch = Backend(_matmul(64, 64, 64)).get_scheduler()
+    for call in (lambda: sch.define_processor_mesh({"x": 2}), lambda: sch.define_memory_mesh({"x": 2}),
+                 lambda: sch.distribute("i", "x"), lambda: sch.distributed_buffer_at("i", 0, ["x"])):
+        with pytest.raises(ScheduleError, match="one GPU"):
+            call()
+
+
+def test_loop_nest():
+    sch = Backend(_matmul(256, 256, 64)).get_scheduler()
+    sch.tile("i", {"i1": 64})
+    sch.interchange(["i", "j", "k", "i1"])
+    nest = sch.get_loop_nest()
+    text = nest.pretty_print() if hasattr(nest, "pretty_print") else str(nest)
+    assert "i1" in str(text)
+
+
+# ---------------------------------------------------------------- mapping
+
+def _sched(graph, tiles=None, order=None, parallel=None):
+    b = Backend(graph)
+    sch = b.get_scheduler()
+    for d, t in (tiles or {}).items():
+        sch.tile(d, t)
+    if order:
+        sch.interchange(order)
+    if parallel:
+        sch.parallelize(parallel)
+    (ln,) = [l for l in b.plan.launches if l.kind in ("matmul", "conv2d")]
+    return ln.attrs, sch.schedule().node(ln.node)
+
+
+def test_mapping_exact_c3a():
+    attrs, s = _sched(_matmul(8192, 8192, 8192, "bfloat16", out_dtype="float32"),
+                      {"i": {"i1": 256, "i2": 64}, "j": {"j1": 256, "j2": 128}, "k": {"k1": 64}})
+    cfg = map_gemm(attrs, False, s, "strict")
+    assert cfg.tile == (256, 256, 64, 4, 2) and cfg.exact and cfg.split_k == 1 and cfg.source == "schedule"
+
+
+def test_mapping_strict_rejects_and_nearest_maps():
+    attrs, s = _sched(_matmul(4096, 4096, 4096), {"i": {"i1": 96}, "j": {"j1": 96}, "k": {"k1": 16}})
+    with pytest.raises(ScheduleError, match="no float32 matmul kernel"):
+        map_gemm(attrs, False, s, "strict")
+    cfg = map_gemm(attrs, False, s, "nearest")
+    assert not cfg.exact and cfg.source == "nearest" and cfg.tile in legal_tiles("float32", False)
+
+
+def test_mapping_split_k():
+    attrs, s = _sched(_matmul(256, 256, 8192), {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 1024, "k2": 32}},
+                      parallel=["k"])
+    cfg = map_gemm(attrs, False, s, "nearest")
+    assert cfg.split_k == 8 and cfg.bk == 32
+    attrs, s = _sched(_matmul(256, 256, 1000), {"k": {"k1": 300}}, parallel=["k"])
+    with pytest.raises(ScheduleError, match="multiple"):
+        map_gemm(attrs, False, s, "nearest")
+
+
+def test_mapping_column_major_raster():
+    g = _matmul(4096, 4096, 4096)
+    attrs, s = _sched(g, {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 16}}, order=["j", "i", "k", "i1", "j1", "k1"])
+    assert map_gemm(attrs, False, s).group_m == 4096 // 128
+    attrs, s = _sched(g, {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 16}})
+    assert map_gemm(attrs, False, s).group_m == 8
+
+
+def test_mapping_default_and_conv_roles():
+    attrs, s = _sched(_matmul(8192, 8192, 8192, "bfloat16", out_dtype="float32"))
+    cfg = map_gemm(attrs, False, s)
+    assert cfg.source == "default" and cfg.tile == (256, 256, 64, 2, 4)
+    # conv: b,h,w tile levels multiply into BM, f is N, r,s,c are K
+    attrs, s = _sched(_conv_relu(), {"h": {"h1": 2}, "w": {"w1": 32}, "f": {"f1": 64}, "c": {"c1": 16}})
+    cfg = map_gemm(attrs, True, s, "nearest")
+    assert cfg.conv and cfg.tile in legal_tiles("float32", True)
+
+
+# ---------------------------------------------------------------- payload codegen
+
+def test_payload_source_and_exports(tmp_path):
+    g = _mlp()
+    b = Backend(g)
+    module = b.get_compiler(dump_file=str(tmp_path / "mlp")).compile(b.get_scheduler().schedule())
+    src = module.source
+    assert "xtc_hip_matmul" in src and "xtc_hip_synchronize" in src
+    syms = subprocess.run(["nm", "-D", "--defined-only", module.file_name], capture_output=True, text=True,
+                          check=True).stdout
+    for sym in ("mlp", "mlp_status", "mlp_message", "mlp_release"):
+        assert re.search(rf"\bT {sym}$", syms, re.M), sym
+    # all scheduled GEMMs carry a kernel choice
+    assert set(module.configs) == {"fc1", "fc2"}
+
+
+def test_concurrent_compiles_share_the_cache():
+    g = _matmul(1024, 1024, 1024)
+    paths, errors = [], []
+
+    def work():
+        try:
+            b = Backend(g)
+            paths.append(b.get_compiler().compile(b.get_scheduler().schedule()).file_name)
+        except Exception as e:  # noqa: BLE001
+            errors.append(e)
+
+    ts = [threading.Thread(target=work) for _ in range(6)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors and len(set(paths)) == 1
+
+
+def test_generated_payload_checks_status_between_launches():
+    b = Backend(_conv_relu())
+    cfgs = b.get_compiler().kernel_configs(b.get_scheduler().schedule())
+    src = generate_payload(b.plan, cfgs, "conv_relu", 0, True)
+    assert src.count("xtc_hip_conv2d(") == 1
+    assert "conv_relu_status" in src and "xtc_hip_synchronize" in src
+    assert "xtc_hip_synchronize" not in generate_payload(b.plan, cfgs, "conv_relu", 0, False).split("conv_relu(")[-1]
+
+
+# ---------------------------------------------------------------- C-ABI library
+
+def _header_functions() -> set[str]:
+    text = (ROOT / "include" / "xtc_hip.h").read_text()
+    return set(re.findall(r"\b(xtc_hip_\w+)\s*\(", text))
+
+
+def test_library_exports_every_declared_function():
+    lib = capi.lib()
+    declared = _header_functions()
+    assert len(declared) >= 25
+    missing = [f for f in declared if not hasattr(lib, f)]
+    assert not missing
+    assert declared == set(capi.SIGNATURES)
+
+
+def test_instances_and_default_tile():
+    inst = capi.gemm_instances()
+    assert len(inst) > 100
+    tiles = {(i["dtype"], bool(i["conv"]), tuple(i["tile"])) for i in inst}
+    assert ("bfloat16", False, (256, 256, 64, 4, 2)) in tiles
+    assert ("bfloat16", False, (256, 256, 64, 2, 4)) in tiles
+    assert any(d == "float32" and c for d, c, _ in tiles)
+    tile, split = capi.default_tile("bfloat16", False, 8192, 8192, 8192)
+    assert tuple(tile) == (256, 256, 64, 2, 4) and split == 1
+
+
+def test_evaluate_flops_is_half_the_flop_rate():
+    lib = capi.lib()
+    assert lib.xtc_hip_evaluate_flops(b"float32") == pytest.approx(157.3e12 / 2)
+    assert lib.xtc_hip_evaluate_flops(b"bfloat16") == pytest.approx(2516.6e12 / 2)
+    assert lib.xtc_hip_evaluate_flops(b"int4") == 0.0
+
+
+def test_device_count_without_gpu_is_safe():
+    n = capi.lib().xtc_hip_device_count()
+    assert n >= 0
+    assert isinstance(capi.lib().xtc_hip_last_error(), (bytes, type(None)))
+    _ = ctypes  # ctypes types come from capi
