@@ -1,0 +1,100 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""loop-explore driver on the CPU: graphs of the CLI, the CSV/DB/manifest
+outputs, resume, and the HIP legality filter.  Evaluation is replaced by a
+stub (no GPU here); compilation runs for real."""
+
+from __future__ import annotations
+
+import csv
+import json
+
+import pytest
+
+from xtc_amd.backends.hip.mapping import map_gemm
+from xtc_amd.cli.explore import DEFAULT_DIMS, build_graph
+from xtc_amd.search.explore import Exploration, ExplorationConfig, hip_sample_filter
+from xtc_amd.search.strategies import Strategies
+
+
+def test_cli_graphs_follow_the_reference_shapes():
+    g = build_graph("conv2d", DEFAULT_DIMS["conv2d"], "float32")
+    # input (n, h*SH + r - 1, w*SW + s - 1, c) (explore.py:253)
+    assert [str(t) for t in g.inputs_types] == ["1x230x230x3xfloat32", "7x7x3x64xfloat32"]
+    assert [str(t) for t in g.outputs_types] == ["1x112x112x64xfloat32"]
+    g = build_graph("conv2d", [8, 56, 56, 64, 3, 3, 64, 1, 1], "float32", pad=1)
+    assert [str(t) for t in g.inputs_types][0] == "8x56x56x64xfloat32"
+    assert [str(t) for t in g.outputs_types] == ["8x56x56x64xfloat32"]
+    g = build_graph("matmul", [16, 8192, 8192], "bfloat16")
+    assert [str(t) for t in g.outputs_types] == ["16x8192xfloat32"]
+    assert build_graph("relu", [1024], "float32").ops_count() == 1024
+
+
+def _stub(monkeypatch, calls):
+    def evaluate_one(self, module):
+        calls.append(module.configs)
+        return [2e-3, 1e-3], 0, ""
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+
+
+def test_run_writes_csv_db_manifest_and_resumes(tmp_path, monkeypatch):
+    calls = []
+    _stub(monkeypatch, calls)
+    g = build_graph("matmul", [512, 512, 512], "float32")
+    out = tmp_path / "r.csv"
+    cfg = ExplorationConfig(trials=5, seed=3, output=str(out), db_file=str(tmp_path / "r.jsonl"),
+                            peak_flops=1e12, jobs=2)
+    res = Exploration(g, cfg).run()
+    assert len(res) == 5 and all(code == 0 for _, _, code, _ in res)
+    rows = list(csv.DictReader(open(out)))
+    assert list(rows[0]) == ["bm", "wm", "bn", "wn", "bk", "split_k", "X", "time", "peak", "backend"]
+    assert len(rows) == 5 and all(float(r["time"]) == 1e-3 for r in rows)
+    # peak = ops_count / peak_flops / time
+    assert float(rows[0]["peak"]) == pytest.approx(512**3 / 1e12 / 1e-3)
+    db = [json.loads(l) for l in open(tmp_path / "r.jsonl")]
+    assert len(db) == 5 and all(d["kernels"]["C"].startswith("gemm<float32>") for d in db)
+    meta = json.loads((tmp_path / "r.csv.meta.json").read_text())
+    assert meta["sampleNames"] == ["bm", "wm", "bn", "wn", "bk", "split_k"] and meta["args"]["trials"] == 5
+    # every sampled schedule compiled to exactly the kernel it names
+    for sample, conf in zip([json.loads(r["X"]) for r in rows], calls):
+        (c,) = conf.values()
+        bm, wm, bn, wn, bk, sk = sample
+        assert (c.bm, c.bn, c.bk, c.bm // c.wgm, c.bn // c.wgn, c.split_k, c.exact) == (bm, bn, bk, wm, wn, sk, True)
+    # resume: the same samples are not run again
+    calls.clear()
+    cfg.resume = True
+    Exploration(g, cfg).run()
+    assert calls == [] and len(list(csv.DictReader(open(out)))) == 5
+    # data search replays the CSV's samples
+    cfg2 = ExplorationConfig(search="data", data=str(out), output=str(tmp_path / "d.csv"), peak_flops=1e12)
+    assert sorted(map(tuple, Exploration(g, cfg2).samples())) == sorted(tuple(json.loads(r["X"])) for r in rows)
+
+
+def test_failed_sample_is_recorded_not_written(tmp_path, monkeypatch):
+    def evaluate_one(self, module):
+        return [], 1, "validation failed"
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    g = build_graph("matmul", [256, 256, 256], "float32")
+    cfg = ExplorationConfig(trials=2, output=str(tmp_path / "f.csv"), db_file=str(tmp_path / "f.jsonl"), peak_flops=1e12)
+    res = Exploration(g, cfg).run()
+    assert [code for _, _, code, _ in res] == [1, 1]
+    assert list(csv.DictReader(open(tmp_path / "f.csv"))) == []
+    assert [json.loads(l)["error"] for l in open(tmp_path / "f.jsonl")] == ["validation failed"] * 2
+
+
+def test_cpu_strategy_samples_are_filtered_to_compiled_kernels():
+    g = build_graph("matmul", [1024, 1024, 1024], "float32")
+    # the CLI's HIP default unroll bound; 256 (the CPU default) excludes every GPU-sized tile
+    ok = hip_sample_filter(g, lambda: Strategies.create("tile_oo", g, max_unroll=1 << 22))
+    st = Strategies.create("tile_oo", g, max_unroll=1 << 22, sample_filter=ok)
+    samples = list(st.sample(8, seed=0))
+    assert len(samples) == 8
+    from xtc_amd.backends.hip import Backend
+
+    for x in samples:
+        b = Backend(g)
+        sch = b.get_scheduler()
+        st.generate(sch, list(x))
+        (ln,) = b.plan.launches
+        assert map_gemm(ln.attrs, False, sch.schedule().node(ln.node), "strict").exact

@@ -23,11 +23,16 @@ from typing import Any
 from ..search.explore import Exploration, ExplorationConfig
 from ..search.strategies import Strategies
 
-DEFAULT_DIMS = {"matmul": [512, 512, 512], "conv2d": [8, 56, 56, 64, 3, 3, 64, 1, 1]}
+# default dims of the reference's OPERATORS table (src/xtc/search/explore.py:150-198)
+DEFAULT_DIMS = {"matmul": [512, 512, 512], "conv2d": [1, 112, 112, 64, 7, 7, 3, 2, 2], "relu": [512 * 1024]}
 
 
 def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0) -> Any:
-    """Graphs of the reference's `--operator` choices (explore.py:151-260)."""
+    """Graphs of the reference's `--operator` choices, with the same tensor
+    and node names and shapes (explore.py:218-256).  bfloat16 matmul/conv
+    accumulate and store fp32 (out_dtype extension).  `pad` > 0 puts a
+    pad2d producer on H and W in front of the conv (the C4 pattern); the
+    padded input then has the reference's conv input shape."""
     import xtc_amd.graphs.xtc.op as O
 
     extra = {"out_dtype": "float32"} if dtype == "bfloat16" else {}
@@ -39,20 +44,26 @@ def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0) -> Any
             O.matmul(a, b, name="C", **extra)
         return gb.graph
     if operator == "conv2d":
-        n, h, w, f, r, s, c, sh, sw = (dims + [1, 1])[:9]
-        ih, iw = (h - 1) * sh + r - 2 * pad, (w - 1) * sw + s - 2 * pad
-        x = O.tensor((n, ih, iw, c), dtype, name="I")
-        wt = O.tensor((r, s, c, f), dtype, name="W")
+        n, h, w, f, r, s, c, sh, sw = dims if len(dims) == 9 else (dims + [1, 1])[:9]
+        ih, iw = h * sh + r - 1 - 2 * pad, w * sw + s - 1 - 2 * pad
+        x = O.tensor((n, ih, iw, c), dtype, name="A")
+        wt = O.tensor((r, s, c, f), dtype, name="B")
         with O.graph(name="conv2d") as gb:
-            src = O.pad2d(x, padding=pad, axes=(1, 2)) if pad else x
-            O.conv2d(src, wt, name="conv", stride=(sh, sw), **extra)
+            src = O.pad2d(x, padding=pad, axes=(1, 2), name="pad") if pad else x
+            O.conv2d(src, wt, stride=(sh, sw), name="O", **extra)
+        return gb.graph
+    if operator == "relu":
+        (i,) = dims
+        x = O.tensor((i,), dtype, name="I")
+        with O.graph(name="relu") as gb:
+            O.relu(x, threshold=0, name="O")
         return gb.graph
     raise SystemExit(f"unknown operator {operator}")
 
 
 def main(argv: list[str] | None = None) -> int:
     p = argparse.ArgumentParser(prog="loop-explore", description=__doc__.split("\n\n")[0])
-    p.add_argument("--operator", default="matmul", choices=["matmul", "conv2d"])
+    p.add_argument("--operator", default="matmul", choices=["matmul", "conv2d", "relu"])
     p.add_argument("--graph-file", help="YAML graph (Graph.dump format) instead of --operator")
     p.add_argument("--dims", nargs="+", type=int, help="operator dimensions")
     p.add_argument("--pad", type=int, default=0, help="conv2d: pad2d producer on H and W")
@@ -64,7 +75,9 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("--trials", type=int, default=64)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--threads", type=int, default=1, help="strategy threads (parallel outer axes)")
-    p.add_argument("--max-unroll", type=int, default=256)
+    p.add_argument("--max-unroll", type=int, default=None,
+                   help="strategy unroll bound (default 2^22: the MFMA kernels always unroll their inner loops, "
+                   "so the CPU bound of 256 would only exclude GPU-sized tiles)")
     p.add_argument("--vec-size", type=int, default=16)
     p.add_argument("--opt-level", type=int, default=2)
     p.add_argument("--repeat", type=int, default=5)
@@ -86,11 +99,12 @@ def main(argv: list[str] | None = None) -> int:
         import xtc_amd.graphs.xtc.op as O
 
         with O.graph() as gb:
-            O.graph.load(args.graph_file)
+            gb.load(args.graph_file)
         graph = gb.graph
     else:
         graph = build_graph(args.operator, args.dims or DEFAULT_DIMS[args.operator], args.dtype, args.pad)
-    strat_kwargs = {"threads": args.threads, "max_unroll": args.max_unroll, "vec_size": args.vec_size}
+    max_unroll = args.max_unroll if args.max_unroll is not None else 1 << 22
+    strat_kwargs = {"threads": args.threads, "max_unroll": max_unroll, "vec_size": args.vec_size}
     if Strategies.resolve_name(args.strategy) == "tile_hip":
         strat_kwargs = {}
     for backend in args.backends:
