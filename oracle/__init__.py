@@ -14,8 +14,11 @@ Contents
   plus the seeded inputs and the tolerance metric used by the parity tests.
 * `cpu_backend` -- C restatement of the compiled MLIR `llvmir` CPU backend
   (tiled loop nest + OpenMP, src/xtc/backends/mlir/MlirCompilerPasses.py and
-  MlirLLVMTarget.py) used as the CPU baseline; built by oracle/Makefile into
-  oracle/_build.
+  MlirLLVMTarget.py) used as the CPU baseline; `cpu_baseline.load()` builds
+  it with -march=native once per host into oracle/_build/<host>/.
+* `Makefile` -- builds the reference's own host runtime (evaluate_perf,
+  CNDArray, evaluate_flops) from its C sources into oracle/_ref/, used by
+  `cpu_baseline` as the timing harness when present.
 
 Pinning (each oracle function is checked against something that is not a
 retyping of its own formula):

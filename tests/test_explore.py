@@ -12,7 +12,7 @@ import pytest
 
 from xtc_amd.backends.hip.mapping import map_gemm
 from xtc_amd.cli.explore import DEFAULT_DIMS, build_graph
-from xtc_amd.search.explore import Exploration, ExplorationConfig, hip_sample_filter
+from xtc_amd.search.explore import Exploration, ExplorationConfig, hip_sample_filter, parse_x
 from xtc_amd.search.strategies import Strategies
 
 
@@ -51,12 +51,20 @@ def test_run_writes_csv_db_manifest_and_resumes(tmp_path, monkeypatch):
     assert len(rows) == 5 and all(float(r["time"]) == 1e-3 for r in rows)
     # peak = ops_count / peak_flops / time
     assert float(rows[0]["peak"]) == pytest.approx(512**3 / 1e12 / 1e-3)
+    assert all(r["X"].count(";") == 5 and "," not in r["X"] for r in rows)
     db = [json.loads(l) for l in open(tmp_path / "r.jsonl")]
     assert len(db) == 5 and all(d["kernels"]["C"].startswith("gemm<float32>") for d in db)
+    # results-DB record of the reference (callback.py:46-60, query_results.py:78-123)
+    d = db[0]
+    assert d["version"] == ["v0.2"] and d["results"] == [0, [1e-3]]
+    assert d["compiler"][0] == "xtc" and d["compiler"][2:] == ["gfx950", 1, "hip"]
+    assert d["operator"][0] == "xtc.graph" and len(d["operator"][1]) == 40 and "name" not in d["operator"][2]
+    assert d["strategy"][0] == "xtc.strategy" and d["strategy"][2] == "tile_hip"
+    assert [x["schedule"] for x in db] == [parse_x(r["X"]) for r in rows]
     meta = json.loads((tmp_path / "r.csv.meta.json").read_text())
     assert meta["sampleNames"] == ["bm", "wm", "bn", "wn", "bk", "split_k"] and meta["args"]["trials"] == 5
     # every sampled schedule compiled to exactly the kernel it names
-    for sample, conf in zip([json.loads(r["X"]) for r in rows], calls):
+    for sample, conf in zip([parse_x(r["X"]) for r in rows], calls):
         (c,) = conf.values()
         bm, wm, bn, wn, bk, sk = sample
         assert (c.bm, c.bn, c.bk, c.bm // c.wgm, c.bn // c.wgn, c.split_k, c.exact) == (bm, bn, bk, wm, wn, sk, True)
@@ -67,7 +75,7 @@ def test_run_writes_csv_db_manifest_and_resumes(tmp_path, monkeypatch):
     assert calls == [] and len(list(csv.DictReader(open(out)))) == 5
     # data search replays the CSV's samples
     cfg2 = ExplorationConfig(search="data", data=str(out), output=str(tmp_path / "d.csv"), peak_flops=1e12)
-    assert sorted(map(tuple, Exploration(g, cfg2).samples())) == sorted(tuple(json.loads(r["X"])) for r in rows)
+    assert sorted(map(tuple, Exploration(g, cfg2).samples())) == sorted(tuple(parse_x(r["X"])) for r in rows)
 
 
 def test_failed_sample_is_recorded_not_written(tmp_path, monkeypatch):
@@ -80,7 +88,9 @@ def test_failed_sample_is_recorded_not_written(tmp_path, monkeypatch):
     res = Exploration(g, cfg).run()
     assert [code for _, _, code, _ in res] == [1, 1]
     assert list(csv.DictReader(open(tmp_path / "f.csv"))) == []
-    assert [json.loads(l)["error"] for l in open(tmp_path / "f.jsonl")] == ["validation failed"] * 2
+    recs = [json.loads(l) for l in open(tmp_path / "f.jsonl")]
+    assert [r["error"] for r in recs] == ["validation failed"] * 2
+    assert [r["results"] for r in recs] == [[1, [0.0]]] * 2
 
 
 def test_cpu_strategy_samples_are_filtered_to_compiled_kernels():

@@ -110,7 +110,9 @@ def test_matmul_c1_seeded_fp32():
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 @pytest.mark.parametrize(
-    "shape", [(21, 32, 16), (100, 72, 40), (1, 8, 8), (257, 136, 64), (33, 264, 520), (5, 4, 3), (7, 6, 5)]
+    "shape",
+    [(21, 32, 16), (100, 72, 40), (1, 8, 8), (257, 136, 64), (33, 264, 520), (5, 4, 3), (7, 6, 5), (9, 17, 1),
+     (4, 1, 7)],
 )
 def test_matmul_ragged(dtype, shape):
     M, N, K = shape

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import csv
+import hashlib
 import json
 import logging
 import os
@@ -36,7 +37,7 @@ from typing import Any, Callable
 
 from .strategies import Strategies
 
-__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter"]
+__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x"]
 
 logger = logging.getLogger("xtc_amd.search")
 
@@ -94,27 +95,68 @@ class CSVCallback:
     def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str) -> None:
         if code != 0 or not times:
             return
+        key = (backend, tuple(int(v) for v in sample))
+        if key in self.seen:
+            return
         t = min(times)
-        self._w.writerow([*sample, str(list(sample)), t, self._peak_time / t if t > 0 else 0.0, backend])
+        # X keeps the sample in one field: list separators become ';'
+        x = str([int(v) for v in sample]).replace(",", ";")
+        self._w.writerow([*sample, x, t, self._peak_time / t if t > 0 else 0.0, backend])
         self._f.flush()
-        self.seen.add((backend, tuple(sample)))
+        self.seen.add(key)
 
     def close(self) -> None:
         self._f.close()
 
 
-class DBCallback:
-    """JSON-lines record per sample (successes and failures)."""
+def parse_x(text: str) -> list[int]:
+    """The X column back to a sample ('[1; 2; 3]' or '[1, 2, 3]')."""
+    return [int(v) for v in json.loads(text.replace(";", ","))]
 
-    def __init__(self, fname: str, graph_name: str, strategy: str) -> None:
+
+DB_VERSION = "v0.2"
+
+
+def db_operator(graph: Any) -> list[Any]:
+    """["xtc.graph", sha1 of the graph dict without its name, the dict]."""
+    obj = graph.to_dict()
+    obj.pop("name", None)
+    return ["xtc.graph", hashlib.sha1(json.dumps(obj).encode()).hexdigest(), obj]
+
+
+def db_strategy(name: str) -> list[Any]:
+    return ["xtc.strategy", hashlib.sha1(json.dumps(name).encode()).hexdigest(), name]
+
+
+class DBCallback:
+    """One JSON line per sample in the results-DB record format of the
+    reference (version, platform, compiler, operator, strategy, schedule,
+    results=[code, [seconds]]; src/xtc/search/callback.py:25-66,
+    src/xtc/cli/query_results.py:25-123); a failed sample records time 0.
+    `kernels` (the kernel instance of each scheduled node) is extra."""
+
+    def __init__(self, fname: str, graph: Any, strategy: str, target: str = "gfx950", threads: int = 1) -> None:
+        from .. import __version__
+
         self._f = open(fname, "a")
-        self._graph = graph_name
-        self._strategy = strategy
+        self._operator = db_operator(graph)
+        self._strategy = db_strategy(strategy)
+        self._platform = [platform.node().split(".")[0], platform.system(), platform.machine()]
+        self._compiler = ["xtc", "v" + __version__, target, threads]
 
     def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str,
                  extra: dict[str, Any] | None = None) -> None:
-        rec = {"graph": self._graph, "strategy": self._strategy, "backend": backend, "sample": list(sample),
-               "results": times, "code": code, "error": msg, **(extra or {})}
+        t = min(times) if (code == 0 and times) else 0.0
+        rec = {
+            "version": [DB_VERSION],
+            "platform": self._platform,
+            "compiler": [*self._compiler, backend],
+            "operator": self._operator,
+            "strategy": self._strategy,
+            "schedule": [int(v) for v in sample],
+            "results": [int(code), [float(t)]],
+            **(extra or {}),
+        }
         self._f.write(json.dumps(rec) + "\n")
         self._f.flush()
 
@@ -176,7 +218,7 @@ class Exploration:
             if not c.data:
                 raise ValueError("search 'data' needs a data CSV")
             with open(c.data, newline="") as f:
-                return [json.loads(row["X"]) for row in csv.DictReader(f)]
+                return [parse_x(row["X"]) for row in csv.DictReader(f)]
         if c.search == "default":
             return [list(self.strategy.default_schedule(c.opt_level))]
         raise ValueError(f"unknown search {c.search!r}")
@@ -227,7 +269,7 @@ class Exploration:
         c = self.config
         samples = self.samples()
         csv_cb = CSVCallback(c.output, self.peak_time(), self.strategy.sample_names, resume=c.resume, append=c.append)
-        db_cb = DBCallback(c.db_file, self.graph.name, c.strategy) if c.db_file else None
+        db_cb = DBCallback(c.db_file, self.graph, c.strategy) if c.db_file else None
         self.write_manifest()
         todo = [s for s in samples if (c.backend, tuple(s)) not in csv_cb.seen]
         results: list[tuple[list[int], list[float], int, str]] = []
@@ -238,7 +280,8 @@ class Exploration:
                 extra: dict[str, Any] = {}
                 try:
                     module = fut.result()
-                    extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()}}
+                    extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()},
+                             "error": ""}
                     times, code, msg = self.evaluate_one(module)
                 except Exception as err:  # a failed sample is recorded, not fatal
                     times, code, msg = [], 2, f"{type(err).__name__}: {err}"
@@ -247,7 +290,7 @@ class Exploration:
                 results.append((sample, times, code, msg))
                 csv_cb(sample, c.backend, times, code, msg)
                 if db_cb:
-                    db_cb(sample, c.backend, times, code, msg, extra)
+                    db_cb(sample, c.backend, times, code, msg, {**extra, "error": msg})
                 best = min(times) if times else 0.0
                 logger.info("[%d/%d] %s -> %.3g s (%s)", idx + 1, len(todo), sample, best, msg or "ok")
         csv_cb.close()
