@@ -81,7 +81,7 @@ def _graph(cfg: str):  # type: ignore[no-untyped-def]
 # level of i/j is the workgroup tile, the second the wave tile, k's first
 # level the LDS slab (xtc_amd/backends/hip/mapping.py).
 SCHEDULES = {
-    "C3a": {"C": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 256, "j2": 128}, "k": {"k1": 64}}},
+    "C3a": {"C": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 64}}},
     "C2": {"C": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 16}}},
 }
 

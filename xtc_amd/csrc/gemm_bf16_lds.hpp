@@ -10,11 +10,12 @@
 //     (global_load_lds_dwordx4): no VGPR staging, no ds_write.  The DMA runs
 //     STAGES-1 slabs ahead of the MFMAs; per slab one s_waitcnt vmcnt(N) for
 //     exactly the slab about to be read, then one barrier.  Measured on
-//     MI355X at 8192^3: the DMA stream alone takes ~720-800 us (~11 TB/s
-//     from L2) against ~450 us of MFMA, so this kernel is bound by the L2
-//     delivery of the A/B panels; BK = 64 with 2 stages beat BK = 32 with 3-5
-//     stages (the per-slab barrier and first LDS reads cost more than the
-//     deeper prefetch gains).
+//     MI355X at 8192^3 (zero inputs, each part alone, the others removed):
+//     MFMA 490 us, DMA 481 us even when every panel read hits L2, LDS
+//     fragment reads 310 us; all together 735 us.  Serving every panel from
+//     L2 saves only 4 %; BK = 32 with 3-5 stages, or a ring of five 32-deep
+//     stages with one barrier per 64 k, was 4-10 % slower than BK = 64 with
+//     2 stages.  The slab's LDS reads and MFMAs are ordered by hand (slab64).
 //   * A stays row-major in LDS (256 rows x 2*BK bytes), read with
 //     ds_read_b128.  The 16-byte chunk of row r is XOR-swizzled by r & 7 for
 //     128-byte rows (BK=64) and by (r >> 1) & 3 for 64-byte rows (BK=32): the
@@ -117,6 +118,64 @@ __device__ __forceinline__ void read_frags(Frags<TM, TN>& f, const unsigned char
     i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
     f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
+}
+
+// One A fragment (one ds_read_b128) / one B fragment (two ds_read_b64_tr_b16)
+// of k-step ks, with the same addressing as read_frags.
+template <int BK, int TM, int TN>
+__device__ __forceinline__ void read_a1(Frags<TM, TN>& f, const unsigned char* sa, int ks, int it, int a_row0, int a_h,
+                                        int g) {
+  const int off = (a_row0 + it * 16) * (2 * BK) + 16 * ((ks * 4 + g) ^ a_h);
+  f.a[it] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sa + off));
+}
+template <int TM, int TN>
+__device__ __forceinline__ void read_b1(Frags<TM, TN>& f, const unsigned char* sb, int ks, int jt, int b_krow0, int b_f,
+                                        int b_c0, int l16) {
+  const int c32 = (b_c0 + jt) ^ b_f;
+  const int off0 = (ks * 32 + b_krow0) * 512 + c32 * 32 + 8 * (l16 & 3);
+  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
+  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
+  f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// The two k-steps of a 64-deep slab in a fixed order (sched_barrier fences
+// keep it): the A fragments and the first LA B fragments of k-step 0; then,
+// per output column jt, the B fragment jt+LA of k-step 0 and a share of
+// k-step 1's fragments followed by the column's TM MFMAs; then all MFMAs of
+// k-step 1, whose operands were read during k-step 0.  Every accumulator
+// sees k-step 0 before k-step 1, as in the plain loop, so results are
+// bit-identical to it.  Left to itself the scheduler issues all 40 reads
+// first and waits for every one of them before the first MFMA (an LDS DMA
+// in flight makes the compiler's LDS waits all-or-nothing).
+template <int BK, int TM, int TN>
+__device__ __forceinline__ void slab64(f32x4 (&acc)[TM][TN], const unsigned char* sa, const unsigned char* sb,
+                                       int a_row0, int a_h, int g, int b_krow0, int b_f, int b_c0, int l16) {
+  constexpr int LA = 2;
+  constexpr int NF1 = TM + TN;  // k-step 1 fragments
+  Frags<TM, TN> f0, f1;
+#pragma unroll
+  for (int it = 0; it < TM; ++it) read_a1<BK>(f0, sa, 0, it, a_row0, a_h, g);
+#pragma unroll
+  for (int jt = 0; jt < LA && jt < TN; ++jt) read_b1(f0, sb, 0, jt, b_krow0, b_f, b_c0, l16);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int jt = 0; jt < TN; ++jt) {
+    if (jt + LA < TN) read_b1(f0, sb, 0, jt + LA, b_krow0, b_f, b_c0, l16);
+#pragma unroll
+    for (int q = jt * NF1 / TN; q < (jt + 1) * NF1 / TN; ++q) {
+      if (q < TM) read_a1<BK>(f1, sa, 1, q, a_row0, a_h, g);
+      else read_b1(f1, sb, 1, q - TM, b_krow0, b_f, b_c0, l16);
+    }
+#pragma unroll
+    for (int it = 0; it < TM; ++it)
+      acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f0.b[jt], f0.a[it], acc[it][jt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int jt = 0; jt < TN; ++jt)
+#pragma unroll
+    for (int it = 0; it < TM; ++it)
+      acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1.b[jt], f1.a[it], acc[it][jt], 0, 0, 0);
 }
 
 template <int TM, int TN>
@@ -236,11 +295,15 @@ gemm_bf16_256x256(BigGemmArgs args) {
     __syncthreads();  // slab kt visible to all waves; stage of slab kt-1 free
     if (kt + STAGES - 1 < nk) issue_slab(kt + STAGES - 1, stages[(s + STAGES - 1) % STAGES]);
     const unsigned char* sa = stages[s];
+    if constexpr (BK == 64) {
+      slab64<BK>(acc, sa, sa + A_STAGE, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
+    } else {
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      Frags<TM, TN> f;
-      read_frags<BK>(f, sa, sa + A_STAGE, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
-      mma(acc, f);
+      for (int ks = 0; ks < BK / 32; ++ks) {
+        Frags<TM, TN> f;
+        read_frags<BK>(f, sa, sa + A_STAGE, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
+        mma(acc, f);
+      }
     }
   };
   for (int kt = 0; kt < nk; kt += STAGES) {
