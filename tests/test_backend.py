@@ -324,3 +324,16 @@ def test_device_count_without_gpu_is_safe():
     assert n >= 0
     assert isinstance(capi.lib().xtc_hip_last_error(), (bytes, type(None)))
     _ = ctypes  # ctypes types come from capi
+
+
+def test_for_node_schedules_several_nodes():
+    b = Backend(_mlp())
+    sch = b.get_scheduler()
+    sch.for_node("fc1").tile("i", {"i1": 256, "i2": 64})
+    sch.for_node("fc2").tile("j", {"j1": 128})
+    s = sch.schedule()
+    assert s.node("fc1").tiles["i"] == {"i1": 256, "i2": 64}
+    assert s.node("fc2").tiles["j"] == {"j1": 128}
+    # a scheduler built on the shared states sees the same schedule
+    other = b.get_scheduler(nodes_schedulers=sch.nodes_schedulers, default_node="fc1")
+    assert other.schedule().node("fc2").tiles["j"] == {"j1": 128}

@@ -108,3 +108,21 @@ def test_cpu_strategy_samples_are_filtered_to_compiled_kernels():
         st.generate(sch, list(x))
         (ln,) = b.plan.launches
         assert map_gemm(ln.attrs, False, sch.schedule().node(ln.node), "strict").exact
+
+
+def test_tile_hip_conv_points_map_exactly():
+    from xtc_amd.backends.hip import Backend
+
+    g = build_graph("conv2d", [8, 56, 56, 64, 3, 3, 64, 1, 1], "float32", pad=1)
+    st = Strategies.create("tile_hip", g)
+    points = list(st.exhaustive())
+    assert len(points) > 10 and all(p[5] == 1 for p in points)
+    for x in points:
+        b = Backend(g)
+        sch = b.get_scheduler()
+        st.generate(sch, list(x))
+        (ln,) = [l for l in b.plan.launches if l.kind == "conv2d"]
+        cfg = map_gemm(ln.attrs, True, sch.schedule().node(ln.node), "strict")
+        assert (cfg.bm, cfg.bm // cfg.wgm, cfg.bn, cfg.bn // cfg.wgn, cfg.bk) == tuple(x[:5])
+    # the default point is the library's own choice
+    assert st.default_schedule(2)[5] >= 1

@@ -279,7 +279,7 @@ def test_memset_zero():
 # ------------------------------------------- LDS-DMA bf16 kernel (256x256x64)
 
 
-def _run_strided(a, b, tile, lda, ldb, ldc, relu=False, bias=None):
+def _run_strided(a, b, tile, lda, ldb, ldc, relu=False, bias=None, split_k=1):
     """bf16 matmul with padded leading dimensions (elements)."""
     M, K = a.shape
     N = b.shape[1]
@@ -296,7 +296,7 @@ def _run_strided(a, b, tile, lda, ldb, ldc, relu=False, bias=None):
     d.M, d.N, d.K = M, N, K
     d.lda, d.ldb, d.ldc = lda, ldb, ldc
     d.tile = capi.Tile(*tile)
-    d.split_k = 1
+    d.split_k = split_k
     d.xcd_remap = 1
     d.relu = int(relu)
     L = capi.lib()
@@ -335,3 +335,36 @@ def test_lds_dma_bf16_swizzle_covers_every_position():
     for waves in ((2, 4), (4, 2)):
         out = run_matmul(a, b, "bfloat16", tile=(256, 256, 64, *waves))
         np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
+
+
+# ------------------------------------------------- skinny bf16 (B-streaming kernel)
+
+SKINNY = (16, 128, 64, 1, 4)
+
+
+@pytest.mark.parametrize("M,N,K,split", [(16, 1024, 8192, 8), (16, 512, 8192, 16), (16, 384, 1024, 1), (5, 256, 2048, 4),
+                                         (1, 128, 512, 1)])
+def test_skinny_bf16_integer_exact(M, N, K, split):
+    # distinct small integers at every (row, k) / (k, col): a wrong swizzle,
+    # transpose, chunk offset or split order changes the exact result
+    a = ((np.arange(M)[:, None] * 5 + np.arange(K)[None, :] * 3) % 7 - 3).astype(np.float32)
+    b = ((np.arange(K)[:, None] * 7 + np.arange(N)[None, :] * 5) % 9 - 4).astype(np.float32)
+    out = run_matmul(a, b, "bfloat16", tile=SKINNY, split_k=split)
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
+
+
+@pytest.mark.parametrize("split", [1, 2])
+def test_skinny_bf16_strided_bias_relu(split):
+    rng = np.random.default_rng(31)
+    M, N, K = 12, 256, 1024 * split
+    a = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    out = _run_strided(a, b, SKINNY, lda=K + 8, ldb=N + 128, ldc=N + 4, relu=True, bias=bias, split_k=split)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_BF16
+
+
+def test_skinny_is_the_default_for_c3b():
+    tile, split = capi.default_tile("bfloat16", False, 16, 8192, 8192)
+    assert tuple(tile) == SKINNY and split == 8

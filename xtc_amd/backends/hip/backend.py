@@ -68,7 +68,12 @@ class HipBackend(Backend):
         return self.node_names[-1]
 
     def get_scheduler(self, **kwargs: Any) -> HipScheduler:
-        return HipScheduler(self, nodes=kwargs.get("nodes"), default_node=kwargs.get("default_node"))
+        return HipScheduler(
+            self,
+            nodes=kwargs.get("nodes"),
+            default_node=kwargs.get("default_node"),
+            nodes_schedulers=kwargs.get("nodes_schedulers"),
+        )
 
     def get_compiler(self, **kwargs: Any) -> HipCompiler:
         return HipCompiler(self, **kwargs)

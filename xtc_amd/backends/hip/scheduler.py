@@ -133,14 +133,20 @@ class HipScheduler(Scheduler):
         backend: "HipBackend",
         nodes: list[str] | None = None,
         default_node: str | None = None,
+        nodes_schedulers: dict[str, "_NodeScheduler"] | None = None,
     ) -> None:
         self._backend = backend
-        names = nodes if nodes is not None else backend.node_names
-        self._schedulers: dict[str, _NodeScheduler] = {}
-        for name in names:
-            op = backend.node_operation(name)
-            dims = list(op.dims)
-            self._schedulers[name] = _NodeScheduler(name, dims, {d: int(v) for d, v in op.dims.items()})
+        if nodes_schedulers is not None:
+            # shares the node states of another scheduler
+            # (MlirScheduler's nodes_schedulers, MlirScheduler.py:22-45)
+            self._schedulers = nodes_schedulers
+        else:
+            names = nodes if nodes is not None else backend.node_names
+            self._schedulers = {}
+            for name in names:
+                op = backend.node_operation(name)
+                dims = list(op.dims)
+                self._schedulers[name] = _NodeScheduler(name, dims, {d: int(v) for d, v in op.dims.items()})
         target = default_node if default_node is not None else backend.default_node
         if target not in self._schedulers:
             raise ScheduleError(f"no schedulable node named {target!r} (nodes: {list(self._schedulers)})")
@@ -153,6 +159,15 @@ class HipScheduler(Scheduler):
     @property
     def node_name(self) -> str:
         return self._current.node_name
+
+    @property
+    def nodes_schedulers(self) -> dict[str, "_NodeScheduler"]:
+        return self._schedulers
+
+    def for_node(self, name: str) -> "HipScheduler":
+        """A scheduler over the same node states whose primitives apply to
+        node `name`: schedules several nodes of one graph."""
+        return HipScheduler(self._backend, default_node=name, nodes_schedulers=self._schedulers)
 
     def schedule(self) -> "HipSchedule":
         return HipSchedule(self, [s.freeze() for s in self._schedulers.values()])

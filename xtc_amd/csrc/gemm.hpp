@@ -205,17 +205,37 @@ gemm_kernel(GemmArgs args) {
   u32x4 areg[P::A_PER_T];
   u32x4 breg[P::B_REGS];
 
+  // conv: when the channel count is a multiple of BK, a slab [kt, kt+BK)
+  // lies in one filter tap (r, s); its coordinates are computed once per
+  // slab from the uniform kt instead of per 16-byte chunk.
+  const bool tap_slabs = CONV && args.cC % BK == 0;
   auto load_a = [&](int kt) {
+    int slab_r = 0, slab_s = 0, slab_c = 0;
+    if constexpr (CONV) {
+      if (tap_slabs) {
+        const int rs = kt / args.cC;
+        slab_c = kt - rs * args.cC;
+        slab_s = rs % args.cS;
+        slab_r = rs / args.cS;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < P::A_PER_T; ++i) {
       int k = kt + a_col[i];
       bool ok = a_rowok[i] && k < k_end;
       if constexpr (CONV) {
         // k -> (r, s, c) in the RSCF weight order
-        int c = k % args.cC;
-        int rs = k / args.cC;
-        int s = rs % args.cS;
-        int r = rs / args.cS;
+        int c, s, r;
+        if (tap_slabs) {
+          c = slab_c + a_col[i];
+          s = slab_s;
+          r = slab_r;
+        } else {
+          c = k % args.cC;
+          const int rs = k / args.cC;
+          s = rs % args.cS;
+          r = rs / args.cS;
+        }
         int ih = a_ih0[i] + r;
         int iw = a_iw0[i] + s;
         bool inb = ok && ih >= 0 && ih < args.cH && iw >= 0 && iw < args.cW;

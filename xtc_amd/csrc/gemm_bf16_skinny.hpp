@@ -1,0 +1,205 @@
+// SPDX-License-Identifier: BSD-3-Clause
+// bf16 GEMM for skinny A (M <= 16 rows) on gfx950: C[M,N] (fp32) =
+// epilogue( A[M,K] (bf16) @ B[K,N] (bf16) ), both row-major.
+//
+// The cost is streaming B (K x N bf16) once from HBM; the arithmetic is a
+// rounding error.  So the kernel is built around the B stream:
+//   * a workgroup owns BN = 128 columns and a KC-deep chunk of K (split-K);
+//     the grid (N/128 x K/KC) gives each CU a few independent 256-byte-wide
+//     B row streams;
+//   * its A slice [16][KC] is copied to LDS once (LDS DMA) and stays there;
+//   * B flows through STAGES LDS stages of 64 k-rows x 256 B by LDS DMA
+//     (global_load_lds_dwordx4), STAGES-1 slabs ahead of the reads, one
+//     vmcnt wait and one barrier per slab;
+//   * 4 waves each own 32 columns; per 32-deep k-step a wave reads one A
+//     fragment (ds_read_b128) and two B fragments (ds_read_b64_tr_b16) and
+//     issues two v_mfma_f32_16x16x32_bf16 (B fragment first, so a lane holds
+//     4 consecutive columns of one row);
+//   * split-K partials go to a workspace [K/KC][M][N]; a second kernel sums
+//     them in split order and applies bias / relu (deterministic).
+// A rows >= M are loaded from row M-1 (any valid row) and never stored.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xtc_hip {
+
+struct SkinnyArgs {
+  const __bf16* A;
+  const __bf16* B;
+  float* W;  // partials [splits][16][ldw], or C itself when splits == 1
+  const float* bias;
+  int M, N, K;
+  int lda, ldb, ldw;
+  int nblocks;  // N / 128
+  int relu;     // epilogue only when the kernel writes C (one split)
+  float relu_threshold;
+};
+
+namespace skinny {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+
+constexpr int BN = 128, BK = 64, WAVES = 4;
+constexpr int B_STAGE = BK * BN * 2;  // 16 KB: 64 k-rows of 256 B
+
+// 32-byte chunk swizzle of a 256-byte B row: the rows 8g + {0..3} and
+// 8g + 8 + {0..3} read by one half-wave land on 8 distinct chunks.
+__device__ __forceinline__ int swz_b(int k) { return (k & 3) | ((k >> 1) & 4); }
+// 16-byte chunk swizzle of an A row (rows are 2*KC bytes apart).
+__device__ __forceinline__ int swz_a(int row) { return row & 7; }
+
+constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+
+}  // namespace skinny
+
+template <int KC, int STAGES>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16_skinny(SkinnyArgs args) {
+  using namespace skinny;
+  constexpr int A_BYTES = 16 * KC * 2;
+  constexpr int A_KB_PER_ROW = 2 * KC / 1024;
+  constexpr int A_DMA_PER_WAVE = 16 * A_KB_PER_ROW / WAVES;
+  constexpr int B_DMA_PER_WAVE = B_STAGE / 1024 / WAVES;  // 4
+  constexpr int NK = KC / BK;
+  static_assert(KC % 512 == 0 && A_DMA_PER_WAVE * WAVES == 16 * A_KB_PER_ROW, "A split");
+  static_assert(STAGES >= 2 && STAGES <= 4 && NK >= STAGES, "stages");
+  static_assert((STAGES - 2) * B_DMA_PER_WAVE < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char sa[A_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char st0[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char st1[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char st2[STAGES > 2 ? B_STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char st3[STAGES > 3 ? B_STAGE : 16];
+  unsigned char* const stages[4] = {st0, st1, st2, st3};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nb = blockIdx.x % args.nblocks;
+  const int split = blockIdx.x / args.nblocks;
+  const int n0 = nb * BN;
+  const int k0 = split * KC;
+
+  // ---- A slice [16][KC] -> LDS, row r at r * 2KC bytes; LDS chunk p of a
+  // row holds global chunk p ^ swz_a(r).
+#pragma unroll
+  for (int i = 0; i < A_DMA_PER_WAVE; ++i) {
+    const int kb = wave * A_DMA_PER_WAVE + i;  // kilobyte of the slice
+    const int r = kb / A_KB_PER_ROW;
+    const int p = (kb % A_KB_PER_ROW) * 64 + lane;
+    const int src_row = r < args.M ? r : args.M - 1;
+    const __bf16* src = args.A + (size_t)src_row * args.lda + k0 + (p ^ swz_a(r)) * 8;
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(sa + kb * 1024), 16, 0, 0);
+  }
+
+  // ---- B slabs: instruction i of wave w fills k-rows 4(4w+i) .. +3 of a
+  // stage; lane l -> row +l/16, 16-byte slot l%16, holding global 32-byte
+  // chunk (slot/2) ^ swz_b(row), half slot%2.
+  int b_off[B_DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < B_DMA_PER_WAVE; ++i) {
+    const int row = 4 * (wave * B_DMA_PER_WAVE + i) + (lane >> 4);
+    const int slot = lane & 15;
+    b_off[i] = row * args.ldb + ((slot >> 1) ^ swz_b(row)) * 16 + (slot & 1) * 8;
+  }
+  const __bf16* b_base = args.B + (size_t)k0 * args.ldb + n0;
+  const size_t b_step = (size_t)BK * args.ldb;
+  auto issue_slab = [&](int kt, unsigned char* st) {
+    const __bf16* bb = b_base + (size_t)kt * b_step;
+#pragma unroll
+    for (int i = 0; i < B_DMA_PER_WAVE; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(bb + b_off[i]),
+                                       (lds_void*)(st + (wave * B_DMA_PER_WAVE + i) * 1024), 16, 0, 0);
+  };
+
+  // ---- fragment coordinates
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int b_krow0 = 8 * g + (l16 >> 2);
+  const int b_f = swz_b(b_krow0);
+  const int b_c0 = wave * 2;  // first 32-byte chunk (16 columns) of the wave
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue_slab(s, stages[s]);
+
+  auto step = [&](int kt, const int s) {
+    // the A slice was issued first, so it has landed whenever slab 0 has
+    if (kt + STAGES - 2 < NK)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * B_DMA_PER_WAVE));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    if (kt + STAGES - 1 < NK) issue_slab(kt + STAGES - 1, stages[(s + STAGES - 1) % STAGES]);
+    const unsigned char* sb = stages[s];
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      const int kk = kt * (BK / 32) + ks;  // 32-deep k-step within the chunk
+      const int aoff = l16 * (2 * KC) + (((kk * 4 + g) ^ swz_a(l16)) * 16);
+      const bf16x8 af = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sa + aoff));
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const int c32 = (b_c0 + jt) ^ b_f;
+        const int off0 = (ks * 32 + b_krow0) * 256 + c32 * 32 + 8 * (l16 & 3);
+        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
+        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 256));
+        const bf16x8 bf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jt], 0, 0, 0);
+      }
+    }
+  };
+  for (int kt = 0; kt < NK; kt += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+      if (kt + s < NK) step(kt + s, s);
+  }
+
+  // ---- store: lane holds row l16, columns n0 + 32 wave + 16 jt + 4g .. +3
+  if (l16 < args.M) {
+    const bool direct = gridDim.x == (unsigned)args.nblocks;  // one split: W is C
+    float* row = args.W + ((direct ? 0 : (size_t)split * 16) + l16) * args.ldw;
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+      const int n = n0 + wave * 32 + jt * 16 + 4 * g;
+      f32x4 v = acc[jt];
+      if (direct) {
+        if (args.bias) v += *(const f32x4*)(args.bias + n);
+        if (args.relu) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = v[r] < args.relu_threshold ? args.relu_threshold : v[r];
+        }
+      }
+      *(f32x4*)(row + n) = v;
+    }
+  }
+}
+
+// C[m][n..n+3] = epilogue( sum_s W[s][m][n..n+3] ), summed in split order.
+// One thread per 4 columns; N % 4 == 0.
+__global__ void skinny_reduce_kernel(const float* __restrict__ W, float* __restrict__ C,
+                                     const float* __restrict__ bias, int M, int N, int ldc, int splits,
+                                     int relu, float thr) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int n4 = N / 4;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * n4) return;
+  const int m = i / n4;
+  const int n = (i - m * n4) * 4;
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) v += *(const f32x4*)(W + ((size_t)s * 16 + m) * N + n);
+  if (bias) v += *(const f32x4*)(bias + n);
+  if (relu) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = v[r] < thr ? thr : v[r];
+  }
+  *(f32x4*)(C + (size_t)m * ldc + n) = v;
+}
+
+}  // namespace xtc_hip

@@ -13,6 +13,7 @@
 #include <string>
 
 #include "gemm_bf16_lds.hpp"
+#include "gemm_bf16_skinny.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
 
@@ -291,6 +292,12 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   const bool f32 = dtype == XTC_HIP_F32;
   const int bk = f32 ? 32 : 64;
   if (M <= 16) {
+    // skinny bf16 with aligned N and K: the B-streaming kernel
+    // (gemm_bf16_skinny.hpp) behind tile 16x128x64, 1x4 waves, 1024-deep splits
+    if (!f32 && N % 128 == 0 && (K % 1024 == 0 || K % 512 == 0) && pick(16, 128, 64, 1, 4)) {
+      *split_k = K % 1024 == 0 ? K / 1024 : K / 512;
+      return;
+    }
     // skinny: stream B once; split K until the grid fills the chip
     int bn = 128;
     if (pick(16, bn, bk, 1, 4) || pick(16, 64, bk, 1, 4)) {
@@ -374,6 +381,67 @@ bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
   // element offsets of one tile row/column range must fit in 32 bits
   if ((int64_t)256 * lda > INT32_MAX || (int64_t)64 * ldb > INT32_MAX) return false;
   return true;
+}
+
+// The skinny bf16 kernel (gemm_bf16_skinny.hpp) implements tile 16x128x64
+// with 1x4 waves for M <= 16 when each split covers 512 or 1024 of K and the
+// shape needs no bounds checks.
+bool skinny_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
+                         int ldb, int ldc, const void* A, const void* B, const void* C,
+                         const void* bias) {
+  static const bool disabled = [] {
+    const char* v = getenv("XTC_HIP_GENERIC_GEMM");
+    return v && v[0] == '1';
+  }();
+  if (disabled || d.dtype != XTC_HIP_BF16) return false;
+  if (t.bm != 16 || t.bn != 128 || t.bk != 64 || t.wgm != 1 || t.wgn != 4) return false;
+  const int splits = split_k < 1 ? 1 : split_k;
+  if (d.M > 16 || d.N % 128 || d.K % splits) return false;
+  const int kc = d.K / splits;
+  if (kc != 512 && kc != 1024) return false;
+  if (lda % 8 || ldb % 8 || ldc % 4) return false;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
+  if ((int64_t)64 * ldb > INT32_MAX) return false;
+  return true;
+}
+
+int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
+                       const void* A, const void* B, float* C, const float* bias, hipStream_t s) {
+  const int splits = split_k < 1 ? 1 : split_k;
+  SkinnyArgs a;
+  a.A = (const __bf16*)A;
+  a.B = (const __bf16*)B;
+  a.bias = bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.nblocks = d.N / 128;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  if (splits == 1) {
+    a.W = C;
+    a.ldw = ldc;
+  } else {
+    size_t bytes = (size_t)splits * 16 * d.N * sizeof(float);
+    a.W = (float*)workspace(bytes);
+    if (!a.W) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
+    a.ldw = d.N;
+  }
+  dim3 grid((unsigned)(a.nblocks * splits));
+  if (d.K / splits == 1024)
+    hipLaunchKernelGGL((gemm_bf16_skinny<1024, 3>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_bf16_skinny<512, 3>), grid, dim3(256), 0, s, a);
+  HIP_TRY(hipGetLastError());
+  if (splits > 1) {
+    const int threads = d.M * (d.N / 4);
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a.W, C, bias,
+                       d.M, d.N, ldc, splits, d.relu, d.relu_threshold);
+    HIP_TRY(hipGetLastError());
+  }
+  return 0;
 }
 
 int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int lda, int ldb,
@@ -614,6 +682,8 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
   if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
     return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s);
+  if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
+    return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = A;

@@ -557,26 +557,43 @@ class Strategy_GOTO_R(Strategy_GOTO):
 class Strategy_HIP(BaseStrategy):
     """GPU space: every compiled GEMM kernel instance of the graph's dtype.
 
-    Sample [bm, wm, bn, wn, bk, split_k] (sizes, not factors) generates
-    tile(i, {i1: bm, i2: wm}), tile(j, {j1: bn, j2: wn}), and on k either
-    {k1: bk} or, with split_k > 1, {k1: K/split_k, k2: bk} plus
-    parallelize(k): the mapping of xtc_amd/backends/hip/mapping.py read
-    backwards.  Matmul only.
+    Sample [bm, wm, bn, wn, bk, split_k] (sizes, not factors); the mapping of
+    xtc_amd/backends/hip/mapping.py read backwards:
+      * matmul (i, j, k): tile(i, {i1: bm, i2: wm}), tile(j, {j1: bn, j2: wn}),
+        and on k either {k1: bk} or, with split_k > 1, {k1: K/split_k, k2: bk}
+        plus parallelize(k);
+      * conv2d (b, h, w, f, r, s, c): the implicit-GEMM rows are b*h*w, so
+        the block and wave heights are split over h and w (w takes up to 8),
+        f carries the block and wave widths and c the slab depth; split_k is 1.
     """
 
     def __init__(self, graph: Any, **kwargs: Any) -> None:
         super().__init__(graph, ["bm", "wm", "bn", "wn", "bk", "split_k"], **kwargs)
         dims = list(self._op.dims)
-        if len(dims) != 3 or list(self._op.dims_kind("R")) != [dims[2]]:
-            raise ValueError("tile_hip applies to matmul-like operations (P, P, R)")
-        self._dims = dims
-        self._M, self._N, self._K = (int(self._op.dims[d]) for d in dims)
+        kinds = [d for d in dims if d in self._op.dims_kind("R")]
         dtype = str(self._op.inputs_types[0].dtype)
         from ..backends.hip.mapping import legal_tiles
 
-        tiles = sorted(set(legal_tiles(dtype, False)))
+        if len(dims) == 3 and kinds == [dims[2]]:
+            self._conv = False
+            self._M, self._N, self._K = (int(self._op.dims[d]) for d in dims)
+        elif len(dims) == 7 and kinds == dims[4:]:
+            self._conv = True
+            size = {d: int(self._op.dims[d]) for d in dims}
+            self._M = size[dims[0]] * size[dims[1]] * size[dims[2]]
+            self._N = size[dims[3]]
+            self._K = size[dims[4]] * size[dims[5]] * size[dims[6]]
+            self._C = size[dims[6]]
+        else:
+            raise ValueError("tile_hip applies to matmul (P, P, R) and conv2d (P, P, P, P, R, R, R) operations")
+        self._dims = dims
+        tiles = sorted(set(legal_tiles(dtype, self._conv)))
         self._tiles = [t for t in tiles if t[0] <= max(16, self._M) * 2 and t[1] <= max(16, self._N) * 2]
-        self._splits = [s for s in (1, 2, 4, 8, 16) if s == 1 or (self._K % s == 0 and self._K // s >= 64)]
+        if self._conv:
+            self._tiles = [t for t in self._tiles if t[2] <= self._C]
+            self._splits = [1]
+        else:
+            self._splits = [s for s in (1, 2, 4, 8, 16) if s == 1 or (self._K % s == 0 and self._K // s >= 64)]
         self._dtype = dtype
 
     def _points(self) -> list[list[int]]:
@@ -599,6 +616,16 @@ class Strategy_HIP(BaseStrategy):
 
     def _generate(self, sch: Any, in_x: list[int]) -> None:
         bm, wm, bn, wn, bk, split = in_x[:6]
+        if self._conv:
+            b, h, w, f, r, s, c = self._dims
+            w1, w2 = min(bm, 8), min(wm, 8)
+            sch.tile(b, {f"{b}1": 1, f"{b}2": 1})
+            sch.tile(h, {f"{h}1": bm // w1, f"{h}2": wm // w2})
+            sch.tile(w, {f"{w}1": w1, f"{w}2": w2})
+            sch.tile(f, {f"{f}1": bn, f"{f}2": wn})
+            sch.tile(c, {f"{c}1": bk})
+            sch.parallelize([b, h, w, f])
+            return
         i, j, k = self._dims
         sch.tile(i, {f"{i}1": bm, f"{i}2": wm})
         sch.tile(j, {f"{j}1": bn, f"{j}2": wn})
@@ -614,7 +641,7 @@ class Strategy_HIP(BaseStrategy):
     def _default_schedule(self, opt_level: int) -> list[int]:
         from ..runtimes.hip import capi
 
-        (bm, bn, bk, wgm, wgn), split = capi.default_tile(self._dtype, False, self._M, self._N, self._K)
+        (bm, bn, bk, wgm, wgn), split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
         return [bm, bm // wgm, bn, bn // wgn, bk, max(1, split)]
 
 
