@@ -60,7 +60,8 @@ def run_matmul(a, b, dtype="float32", tile=None, split_k=0, relu=False, thr=0.0,
     return C.to_numpy((M, N), np.float32)
 
 
-def run_conv(x, w, dtype="float32", stride=(1, 1), pads=(0, 0, 0, 0), pad_value=0.0, tile=None, relu=False, split_k=0):
+def run_conv(x, w, dtype="float32", stride=(1, 1), pads=(0, 0, 0, 0), pad_value=0.0, tile=None, relu=False, split_k=0,
+             bias=None):
     n, h, wd, c = x.shape
     r, s, _, f = w.shape
     I, W = _dev(x, dtype), _dev(w, dtype)
@@ -79,7 +80,9 @@ def run_conv(x, w, dtype="float32", stride=(1, 1), pads=(0, 0, 0, 0), pad_value=
     d.xcd_remap = 1
     d.relu = int(relu)
     L = capi.lib()
-    capi.check(L.xtc_hip_conv2d(ctypes.byref(d), I.c_ptr, W.c_ptr, O.c_ptr, None), "conv2d")
+    bias_buf = DeviceBuffer.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    capi.check(L.xtc_hip_conv2d(ctypes.byref(d), I.c_ptr, W.c_ptr, O.c_ptr, bias_buf.c_ptr if bias_buf else None),
+               "conv2d")
     capi.check(L.xtc_hip_synchronize(), "sync")
     return O.to_numpy((n, oh, ow, f), np.float32)
 
@@ -368,3 +371,53 @@ def test_skinny_bf16_strided_bias_relu(split):
 def test_skinny_is_the_default_for_c3b():
     tile, split = capi.default_tile("bfloat16", False, 16, 8192, 8192)
     assert tuple(tile) == SKINNY and split == 8
+
+
+# ------------------------------------------- direct conv (fp32, C and F multiples of 64)
+
+DIRECT = (64, 64, 16, 2, 2)
+
+
+def _int_tensor(shape, mul, mod):
+    idx = np.indices(shape).reshape(len(shape), -1)
+    v = (sum((i + 1) * mul[j] for j, i in enumerate(idx)) % mod) - mod // 2
+    return v.reshape(shape).astype(np.float32)
+
+
+@pytest.mark.parametrize(
+    "n,h,w,c,f,r,s,pads,pad_value",
+    [
+        (2, 13, 11, 64, 128, 3, 3, (1, 1, 1, 1), 0.0),   # partial 8x8 blocks, two filter blocks
+        (1, 9, 10, 128, 64, 3, 3, (2, 0, 1, 3), 1.0),    # two channel chunks, asymmetric pads, pad value
+        (3, 8, 8, 64, 64, 1, 1, (0, 0, 0, 0), 0.0),      # 1x1
+        (1, 6, 7, 64, 64, 4, 2, (1, 2, 0, 1), -2.0),     # 4x2 window
+    ],
+)
+def test_direct_conv_integer_exact(n, h, w, c, f, r, s, pads, pad_value):
+    x = _int_tensor((n, h, w, c), (3, 5, 7, 1), 7)
+    wt = _int_tensor((r, s, c, f), (2, 3, 1, 5), 5)
+    out = run_conv(x, wt, pads=pads, pad_value=pad_value, tile=DIRECT)
+    xp = ref.pad(x, [(0, 0), pads[:2], pads[2:], (0, 0)], pad_value)
+    np.testing.assert_array_equal(out, ref.conv2d(xp, wt).astype(np.float32))
+
+
+def test_direct_conv_bias_relu_seeded():
+    rng = np.random.default_rng(41)
+    x = rng.uniform(0, 1, (2, 14, 14, 64)).astype(np.float32)
+    wt = rng.normal(0, 0.06, (3, 3, 64, 64)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, (64,)).astype(np.float32)
+    out = run_conv(x, wt, pads=(1, 1, 1, 1), tile=DIRECT, relu=True, bias=bias)
+    xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    expect = ref.relu(ref.conv2d(xp, wt) + bias)
+    assert ref.scaled_error(out, expect, 576, 1.0, np.abs(wt).max()) <= TOL_F32
+
+
+def test_direct_conv_is_the_default_for_c4_and_strided_falls_back():
+    tile, split = capi.default_tile("float32", True, 8 * 56 * 56, 64, 576)
+    assert tuple(tile) == DIRECT and split == 1
+    # stride 2: the 8x8 block's halo exceeds the LDS buffer -> implicit-GEMM kernel, same tile
+    x = _int_tensor((1, 20, 20, 64), (3, 5, 7, 1), 7)
+    wt = _int_tensor((3, 3, 64, 64), (2, 3, 1, 5), 5)
+    out = run_conv(x, wt, stride=(2, 2), pads=(1, 1, 1, 1), tile=DIRECT)
+    xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    np.testing.assert_array_equal(out, ref.conv2d(xp, wt, (2, 2)).astype(np.float32))

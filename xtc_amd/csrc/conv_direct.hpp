@@ -1,0 +1,218 @@
+// SPDX-License-Identifier: BSD-3-Clause
+// Direct NHWC x RSCF conv2d (fp32) on gfx950 for channel counts that are
+// multiples of 64:
+//   O[b,oh,ow,f] = epilogue( sum_{r,s,c} Ipad[b, oh*sh+r, ow*sw+s, c] * W[r,s,c,f] )
+// with the pad of a pad2d producer folded in (out-of-image taps read
+// pad_value), as XTCOperConv2D after XTCOperPad2D (operators.py:252-347,
+// 350-591).
+//
+// Why not the implicit-GEMM loader: for shapes like 8x56x56x64 * 3x3x64x64
+// (GEMM M=25088, N=64, K=576) each tile walks only K=576 and re-reads every
+// input pixel once per filter tap from L2; the global-load latency is then
+// exposed on every slab.  Here a workgroup owns an 8x8 block of output
+// pixels x 64 filters of one image:
+//   * the input halo ((8-1)*sh+R) x ((8-1)*sw+S) pixels x 64 channels is
+//     loaded once into LDS (pad_value outside the image), pixel stride 68
+//     floats so the 16 pixels read by a lane group fall on distinct banks;
+//   * the weights stream one tap (r, s) [64 c][64 f] = 16 KB at a time
+//     through 3 LDS stages by LDS DMA, two taps ahead; the 16-byte chunks of
+//     weight row c are XOR-swizzled by 4*((c>>2)&3) so the scalar B reads of
+//     the four lane groups hit disjoint banks;
+//   * 4 waves (2x2), each 32 pixels x 32 filters of v_mfma_f32_16x16x4_f32;
+//     the filter fragment is the first operand, so a lane ends up with 4
+//     consecutive filters of one pixel and stores a float4;
+//   * more than 64 channels: the halo is reloaded per 64-channel chunk.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xtc_hip {
+
+struct DirectConvArgs {
+  const float* I;  // [NB][H][W][C], unpadded
+  const float* Wt;  // [R][S][C][F]
+  float* O;        // [NB][OH][OW][F]
+  const float* bias;
+  int NB, H, W, C, F, R, S;
+  int sh, sw;
+  int pt, pl;      // top / left padding
+  int OH, OW;
+  float pad_value;
+  int relu;
+  float relu_threshold;
+  int tiles_h, tiles_w;  // ceil(OH/8), ceil(OW/8)
+};
+
+namespace dconv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int TH = 8, TW = 8;     // output pixels per workgroup
+constexpr int CB = 64;            // channels per chunk
+constexpr int FB = 64;            // filters per workgroup
+constexpr int CP = CB + 4;        // halo pixel stride (floats)
+constexpr int W_STAGE = CB * FB * 4;  // 16 KB
+constexpr int STAGES = 3;
+constexpr int HALO_MAX_BYTES = 32 * 1024;
+constexpr int HALO_MAX_PIX = HALO_MAX_BYTES / (CP * 4);  // 120 pixels
+constexpr int DMA_PER_WAVE = W_STAGE / 1024 / 4;          // 4
+
+__device__ __forceinline__ int swz(int c) { return 4 * ((c >> 2) & 3); }
+constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+
+}  // namespace dconv
+
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_direct_f32(DirectConvArgs a) {
+  using namespace dconv;
+  __shared__ __attribute__((aligned(1024))) float halo[HALO_MAX_PIX * CP];
+  __shared__ __attribute__((aligned(1024))) unsigned char w0[W_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char w1[W_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char w2[W_STAGE];
+  unsigned char* const wst[3] = {w0, w1, w2};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;  // pixel half: pixels 32 wm .. +31
+  const int wn = wave & 1;   // filter half: filters 32 wn .. +31
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+
+  // block -> (image, tile row, tile column, filter block); filters fastest
+  const int fblocks = a.F / FB;
+  int bid = blockIdx.x;
+  const int fb = bid % fblocks;
+  bid /= fblocks;
+  const int tw = bid % a.tiles_w;
+  bid /= a.tiles_w;
+  const int th = bid % a.tiles_h;
+  const int img = bid / a.tiles_h;
+  const int oh0 = th * TH, ow0 = tw * TW;
+  const int HH = (TH - 1) * a.sh + a.R;
+  const int HW = (TW - 1) * a.sw + a.S;
+  const int ih0 = oh0 * a.sh - a.pt;
+  const int iw0 = ow0 * a.sw - a.pl;
+  const int taps = a.R * a.S;
+  const int chunks = a.C / CB;
+  const int nslab = chunks * taps;  // weight slabs, chunk-major
+
+  // weight slab t = (chunk, tap): rows c of W[r][s][chunk*64 + c][fb*64 ..]
+  int w_row[DMA_PER_WAVE], w_col[DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < DMA_PER_WAVE; ++i) {
+    const int c = 4 * (wave * DMA_PER_WAVE + i) + (lane >> 4);
+    w_row[i] = c;
+    w_col[i] = fb * FB + ((lane & 15) ^ swz(c)) * 4;
+  }
+  auto issue_slab = [&](int t, unsigned char* st) {
+    const int chunk = t / taps;
+    const int tap = t - chunk * taps;
+    const float* base = a.Wt + ((size_t)tap * a.C + chunk * CB) * a.F;
+#pragma unroll
+    for (int i = 0; i < DMA_PER_WAVE; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(base + (size_t)w_row[i] * a.F + w_col[i]),
+                                       (lds_void*)(st + (wave * DMA_PER_WAVE + i) * 1024), 16, 0, 0);
+  };
+
+  auto load_halo = [&](int chunk) {
+    const int n16 = HH * HW * (CB / 4);  // 16-byte chunks
+    for (int q = tid; q < n16; q += 256) {
+      const int pix = q >> 4;
+      const int cc = (q & 15) * 4;
+      const int hy = pix / HW, hx = pix - (pix / HW) * HW;
+      const int ih = ih0 + hy, iw = iw0 + hx;
+      f32x4 v;
+      if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+        v = *(const f32x4*)(a.I + (((size_t)img * a.H + ih) * a.W + iw) * a.C + chunk * CB + cc);
+      else
+        v = f32x4{a.pad_value, a.pad_value, a.pad_value, a.pad_value};
+      *(f32x4*)(halo + pix * CP + cc) = v;
+    }
+  };
+
+  // output pixels of this lane's two 16-pixel tiles
+  int php[2], pwp[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int p = wm * 32 + it * 16 + l16;
+    php[it] = p / TW;
+    pwp[it] = p % TW;
+  }
+
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < nslab) issue_slab(t, wst[t]);
+
+  auto step = [&](int t, const int s) {
+    const int chunk = t / taps;
+    const int tap = t - chunk * taps;
+    if (tap == 0) {
+      if (chunk > 0) __syncthreads();  // every wave is done with the previous chunk's halo
+      load_halo(chunk);
+    }
+    if (t + STAGES - 2 < nslab)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * DMA_PER_WAVE));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();  // slab t (and the halo) visible; stage of slab t-1 free
+    if (t + STAGES - 1 < nslab) issue_slab(t + STAGES - 1, wst[(s + STAGES - 1) % STAGES]);
+    const float* ws = (const float*)wst[s];
+    const int r = tap / a.S;
+    const int sx = tap - r * a.S;
+    int aoff[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) aoff[it] = ((php[it] * a.sh + r) * HW + pwp[it] * a.sw + sx) * CP + 4 * g;
+#pragma unroll
+    for (int kc = 0; kc < CB / 16; ++kc) {
+      f32x4 av[2];
+#pragma unroll
+      for (int it = 0; it < 2; ++it) av[it] = *(const f32x4*)(halo + aoff[it] + kc * 16);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int c = kc * 16 + 4 * g + st;
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          const int f = wn * 32 + jt * 16 + l16;
+          const float bv = ws[c * FB + ((f >> 2) ^ swz(c)) * 4 + (f & 3)];
+#pragma unroll
+          for (int it = 0; it < 2; ++it)
+            acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av[it][st], acc[it][jt], 0, 0, 0);
+        }
+      }
+    }
+  };
+  for (int t = 0; t < nslab; t += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+      if (t + s < nslab) step(t + s, s);
+  }
+
+  // lane holds filters f0 .. f0+3 of pixel (php, pwp) for each (it, jt)
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int oh = oh0 + php[it], ow = ow0 + pwp[it];
+    if (oh >= a.OH || ow >= a.OW) continue;
+    float* out = a.O + (((size_t)img * a.OH + oh) * a.OW + ow) * a.F + fb * FB;
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+      const int f = wn * 32 + jt * 16 + 4 * g;
+      f32x4 v = acc[it][jt];
+      if (a.bias) v += *(const f32x4*)(a.bias + fb * FB + f);
+      if (a.relu) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = v[q] < a.relu_threshold ? a.relu_threshold : v[q];
+      }
+      *(f32x4*)(out + f) = v;
+    }
+  }
+}
+
+}  // namespace xtc_hip

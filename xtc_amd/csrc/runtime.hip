@@ -14,6 +14,7 @@
 
 #include "gemm_bf16_lds.hpp"
 #include "gemm_bf16_skinny.hpp"
+#include "conv_direct.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
 
@@ -291,6 +292,7 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   };
   const bool f32 = dtype == XTC_HIP_F32;
   const int bk = f32 ? 32 : 64;
+  if (conv && f32 && N % 64 == 0 && K % 64 == 0 && pick(64, 64, 16, 2, 2)) return;
   if (M <= 16) {
     // skinny bf16 with aligned N and K: the B-streaming kernel
     // (gemm_bf16_skinny.hpp) behind tile 16x128x64, 1x4 waves, 1024-deep splits
@@ -441,6 +443,57 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
                        d.M, d.N, ldc, splits, d.relu, d.relu_threshold);
     HIP_TRY(hipGetLastError());
   }
+  return 0;
+}
+
+// The direct conv kernel (conv_direct.hpp) implements the conv tile 64x64x16
+// with 2x2 waves for fp32 when C and F are multiples of 64 and the input
+// halo of an 8x8 output block fits its LDS buffer.
+bool direct_conv_applies(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int split_k, int OH, int OW,
+                         const void* I, const void* W, const void* O, const void* bias) {
+  static const bool disabled = [] {
+    const char* v = getenv("XTC_HIP_GENERIC_GEMM");
+    return v && v[0] == '1';
+  }();
+  if (disabled || d.dtype != XTC_HIP_F32 || split_k > 1) return false;
+  if (t.bm != 64 || t.bn != 64 || t.bk != 16 || t.wgm != 2 || t.wgn != 2) return false;
+  if (d.C % 64 || d.F % 64) return false;
+  const int hh = 7 * d.stride_h + d.R, hw = 7 * d.stride_w + d.S;
+  if (hh * hw > dconv::HALO_MAX_PIX) return false;
+  if (!aligned16(I) || !aligned16(W) || !aligned16(O) || (bias && !aligned16(bias))) return false;
+  if ((int64_t)d.R * d.S * d.C * d.F > INT32_MAX || (int64_t)d.N * OH * OW > INT32_MAX) return false;
+  return true;
+}
+
+int launch_direct_conv(const xtc_hip_conv2d_desc& d, int OH, int OW, const void* I, const void* W, float* O,
+                       const float* bias, hipStream_t s) {
+  DirectConvArgs a;
+  a.I = (const float*)I;
+  a.Wt = (const float*)W;
+  a.O = O;
+  a.bias = bias;
+  a.NB = d.N;
+  a.H = d.H;
+  a.W = d.W;
+  a.C = d.C;
+  a.F = d.F;
+  a.R = d.R;
+  a.S = d.S;
+  a.sh = d.stride_h;
+  a.sw = d.stride_w;
+  a.pt = d.pad_top;
+  a.pl = d.pad_left;
+  a.OH = OH;
+  a.OW = OW;
+  a.pad_value = d.pad_value;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  a.tiles_h = (OH + dconv::TH - 1) / dconv::TH;
+  a.tiles_w = (OW + dconv::TW - 1) / dconv::TW;
+  const uint64_t blocks = (uint64_t)d.N * a.tiles_h * a.tiles_w * (d.F / dconv::FB);
+  if (blocks > 0x7fffffffu) return fail("conv2d grid too large");
+  hipLaunchKernelGGL(conv_direct_f32, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  HIP_TRY(hipGetLastError());
   return 0;
 }
 
@@ -748,6 +801,8 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   if (!e)
     return fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  if (direct_conv_applies(d, t, split_k, OH, OW, input, weight, out, bias))
+    return launch_direct_conv(d, OH, OW, input, weight, out, bias, s);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = input;
