@@ -89,6 +89,8 @@ class _NodeScheduler:
         self.packed_buffers: dict[str, list[int]] = {}
         self.buffers: list[str] = []
         self.fused: list[tuple[str, int]] = []
+        self.buffer_at: dict[str, str | None] = {}
+        self.pack_at: dict[str, tuple[int, str | None, bool]] = {}
 
     def _dim_of(self, name: str) -> str:
         if name in self.dims:
@@ -211,9 +213,10 @@ class HipScheduler(Scheduler):
             self._current.unrolling[loop_name(root, name)] = int(factor)
 
     def buffer_at(self, axis: str, mtype: str | None = None, root: str = DEFAULT_ROOT) -> None:
-        if mtype not in (None, "global", "local"):
+        if mtype not in (None, "global", "local", "shared"):
             raise ScheduleError(f"buffer_at: unknown memory type {mtype!r}")
         self._current.buffers.append(loop_name(root, axis))
+        self._current.buffer_at[loop_name(root, axis)] = mtype
 
     def pack_at(
         self,
@@ -223,9 +226,10 @@ class HipScheduler(Scheduler):
         pad: bool = False,
         root: str = DEFAULT_ROOT,
     ) -> None:
-        if mtype not in (None, "global", "local"):
+        if mtype not in (None, "global", "local", "shared"):
             raise ScheduleError(f"pack_at: unknown memory type {mtype!r}")
         self._current.packed_buffers.setdefault(loop_name(root, axis), []).append(int(input_idx))
+        self._current.pack_at[loop_name(root, axis)] = (int(input_idx), mtype, pad)
 
     def fuse_producer_at(self, axis: str, input_idx: int, root: str = DEFAULT_ROOT) -> None:
         self._current.fused.append((loop_name(root, axis), int(input_idx)))
@@ -251,37 +255,50 @@ class HipScheduler(Scheduler):
         self._single_gpu("distributed_buffer_at")
 
     def get_loop_nest(self) -> LoopNest:
-        sched = self._current.freeze()
-        nest = LoopNest(abstract_dims=list(sched.dims), sizes=dict(sched.sizes))
-        root = nest.build_root_node(sched.node_name)
-        for dim, segs in sched.splits.items():
-            root.splits[dim] = {basename(k): v for k, v in segs.items()}
-        seg_origin: dict[str, SplitOrigin] = {}
-        for dim, segs in sched.splits.items():
+        """The current node's schedule as a LoopNest: the root "." and one
+        child per split segment, each with its own tiles, loop order and
+        annotations, loop names without their root prefix."""
+        cur = self._current
+        sched = cur.freeze()
+        nest = LoopNest(abstract_dims=list(sched.dims))
+        root = nest.build_root_node(DEFAULT_ROOT)
+        segments: dict[str, tuple[str, SplitOrigin]] = {}  # qualified segment -> (dim, origin)
+        for dim, segs in cur.splits.items():
             names = list(segs)
             for idx, seg in enumerate(names):
                 end = segs[names[idx + 1]] if idx + 1 < len(names) else None
-                seg_origin[basename(seg)] = SplitOrigin(axis=dim, start=segs[seg], end=end)
+                segments[seg] = (dim, SplitOrigin(axis=dim, start=segs[seg], end=end))
 
-        def fill(node: LoopNestNode, perm: list[str]) -> None:
+        def parent_of(qualified: str) -> str:
+            return qualified.rsplit("/", 1)[0]
+
+        def fill(node: LoopNestNode, root_name: str) -> None:
+            perm = sched.permutation.get(root_name)
+            if perm is None:
+                perm = cur.default_interchange(root_name) if root_name == DEFAULT_ROOT else []
             members = set(perm)
             node.interchange = [basename(p) for p in perm]
-            for dim, levels in self._current.tiles.items():
+            for dim, levels in cur.tiles.items():
+                if dim not in sched.dims:
+                    continue
                 for name, size in levels.items():
-                    if name in members:
+                    if parent_of(name) == root_name:
                         node.tiles.setdefault(dim, {})[basename(name)] = size
+            for seg, (dim, _) in segments.items():
+                if parent_of(seg) == root_name:
+                    node.splits.setdefault(dim, {})[basename(seg)] = cur.splits[dim][seg]
             node.vectorize = [basename(v) for v in sched.vectorization if v in members]
-            node.parallelize = [basename(p) for p in sched.parallelization if p in members]
+            node.parallelize = [basename(v) for v in sched.parallelization if v in members]
             node.unroll = {basename(k): v for k, v in sched.unrolling.items() if k in members}
+            node.buffer_at = {basename(k): v for k, v in cur.buffer_at.items() if k in members}
+            node.pack_at = {basename(k): v for k, v in cur.pack_at.items() if k in members}
+            for seg, (dim, origin) in segments.items():
+                if parent_of(seg) == root_name:
+                    child = LoopNestNode(root=seg, tiles={d: {} for d in sched.dims}, split_origin=origin)
+                    node.add_child(child)
+                    fill(child, seg)
 
-        for r, perm in sched.permutation.items():
-            name = basename(r)
-            if name in seg_origin:
-                child = LoopNestNode(root=name, tiles={d: {} for d in sched.dims}, split_origin=seg_origin[name])
-                fill(child, perm)
-                root.add_child(child)
-            else:
-                fill(root, perm)
+        fill(root, DEFAULT_ROOT)
         return nest
 
 
