@@ -165,6 +165,38 @@ def test_matmul_split_k_bias_relu(dtype):
     assert (out >= 0).all()
 
 
+def _int_operands(M, N, K, seed):
+    a = ((np.arange(M)[:, None] * (3 + seed) + np.arange(K)[None, :] * 5) % 7 - 3).astype(np.float32)
+    b = ((np.arange(K)[:, None] * 11 + np.arange(N)[None, :] * (2 + seed)) % 9 - 4).astype(np.float32)
+    return a, b
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_split_k_in_kernel_reduction_back_to_back(dtype):
+    # The last workgroup of each output tile sums the partials and resets the
+    # tile's arrival counter.  Back-to-back calls with other data, other tile
+    # counts and other split counts only come out exact if every call leaves
+    # the counters at zero; the ragged shapes (N % 4 != 0, partial tiles) take
+    # the scalar finishing path, the aligned ones the float4 path.
+    cases = [(70, 130, 1536, 3, 0), (64, 128, 4096, 4, 1), (70, 130, 1536, 3, 2), (33, 257, 2048, 8, 3),
+             (64, 128, 4096, 2, 4)]
+    for M, N, K, split, seed in cases:
+        a, b = _int_operands(M, N, K, seed)
+        bias = (np.arange(N) % 5 - 2).astype(np.float32)
+        out = run_matmul(a, b, dtype, split_k=split, relu=True, thr=1.0, bias=bias)
+        expect = ref.relu(ref.matmul(a, b) + bias, 1.0).astype(np.float32)
+        np.testing.assert_array_equal(out, expect, err_msg=f"{dtype} {(M, N, K)} split {split}")
+
+
+def test_split_k_conv_in_kernel_reduction():
+    x = ((np.arange(2 * 9 * 11 * 24).reshape(2, 9, 11, 24) * 7) % 5 - 2).astype(np.float32)
+    w = ((np.arange(3 * 3 * 24 * 20).reshape(3, 3, 24, 20) * 3) % 7 - 3).astype(np.float32)
+    expect = ref.conv2d(x, w).astype(np.float32)
+    for _ in range(2):
+        out = run_conv(x, w, split_k=3)
+        np.testing.assert_array_equal(out, expect)
+
+
 def test_matmul_relu_threshold_nan():
     a = np.ones((16, 8), np.float32)
     b = np.ones((8, 16), np.float32)

@@ -30,10 +30,13 @@
 //   * Grid: 1-D over tiles, remapped so each XCD owns a contiguous range of
 //     tiles, then grouped (GROUP_M tile rows) for L2 reuse; z = split-K.
 //   * Epilogue: optional bias[N] and relu fused; split-K writes fp32 partial
-//     sums to a workspace and a reduce kernel applies the epilogue.
+//     sums to a workspace and the workgroup that stores a tile's last partial
+//     sums them in split order and applies the epilogue (splitk.hpp).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "splitk.hpp"
 
 namespace xtc_hip {
 
@@ -47,6 +50,7 @@ struct GemmArgs {
   float* C;           // [M][ldc]
   const float* bias;  // [N] or null
   float* partial;     // split-K workspace [splits][M][N] or null
+  unsigned* counters; // split-K arrival counters [tiles_m * tiles_n], zero between launches
   int M, N, K;
   int lda, ldb, ldc;
   int k_per_split;    // multiple of BK
@@ -417,10 +421,18 @@ gemm_kernel(GemmArgs args) {
             v += bv;
             if (args.relu && v < args.relu_threshold) v = args.relu_threshold;
           }
-          out[(size_t)row * ldo + col] = v;
+          if (to_partial)
+            splitk_store(out + (size_t)row * ldo + col, v);
+          else
+            out[(size_t)row * ldo + col] = v;
         }
       }
     }
+  }
+  if (to_partial && splitk_arrive(args.counters + tile_m * args.tiles_n + tile_n, (int)gridDim.z)) {
+    splitk_finish_tile<BM, BN, NT>(args.partial, args.C, args.bias, args.M, args.N, args.ldc, (int)gridDim.z,
+                                   args.relu, args.relu_threshold, m0, n0);
+    splitk_release(args.counters + tile_m * args.tiles_n + tile_n);
   }
 }
 

@@ -15,12 +15,16 @@
 //     fragment (ds_read_b128) and two B fragments (ds_read_b64_tr_b16) and
 //     issues two v_mfma_f32_16x16x32_bf16 (B fragment first, so a lane holds
 //     4 consecutive columns of one row);
-//   * split-K partials go to a workspace [K/KC][M][N]; a second kernel sums
-//     them in split order and applies bias / relu (deterministic).
+//   * split-K partials go to a workspace [K/KC][16][N] (agent-scope stores);
+//     the workgroup that stores the last partial of a column block sums them
+//     in split order and applies bias / relu (splitk.hpp), so the result is
+//     deterministic and the GEMM stays one launch.
 // A rows >= M are loaded from row M-1 (any valid row) and never stored.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "splitk.hpp"
 
 namespace xtc_hip {
 
@@ -28,11 +32,13 @@ struct SkinnyArgs {
   const __bf16* A;
   const __bf16* B;
   float* W;  // partials [splits][16][ldw], or C itself when splits == 1
+  float* C;  // [M][ldc]
   const float* bias;
+  unsigned* counters;  // [nblocks] arrival counters, zero between launches
   int M, N, K;
-  int lda, ldb, ldw;
+  int lda, ldb, ldw, ldc;
   int nblocks;  // N / 128
-  int relu;     // epilogue only when the kernel writes C (one split)
+  int relu;
   float relu_threshold;
 };
 
@@ -162,8 +168,9 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
   }
 
   // ---- store: lane holds row l16, columns n0 + 32 wave + 16 jt + 4g .. +3
+  const int splits = gridDim.x / args.nblocks;
+  const bool direct = splits == 1;  // W is C
   if (l16 < args.M) {
-    const bool direct = gridDim.x == (unsigned)args.nblocks;  // one split: W is C
     float* row = args.W + ((direct ? 0 : (size_t)split * 16) + l16) * args.ldw;
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
@@ -176,30 +183,32 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
           for (int r = 0; r < 4; ++r) v[r] = v[r] < args.relu_threshold ? args.relu_threshold : v[r];
         }
       }
-      *(f32x4*)(row + n) = v;
+      if (direct)
+        *(f32x4*)(row + n) = v;
+      else
+        splitk_store4(row + n, v);
     }
   }
-}
+  if (direct || !splitk_arrive(args.counters + nb, splits)) return;
 
-// C[m][n..n+3] = epilogue( sum_s W[s][m][n..n+3] ), summed in split order.
-// One thread per 4 columns; N % 4 == 0.
-__global__ void skinny_reduce_kernel(const float* __restrict__ W, float* __restrict__ C,
-                                     const float* __restrict__ bias, int M, int N, int ldc, int splits,
-                                     int relu, float thr) {
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  const int n4 = N / 4;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M * n4) return;
-  const int m = i / n4;
-  const int n = (i - m * n4) * 4;
-  f32x4 v = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) v += *(const f32x4*)(W + ((size_t)s * 16 + m) * N + n);
-  if (bias) v += *(const f32x4*)(bias + n);
-  if (relu) {
+  // ---- last workgroup of the column block: C[m][n0 + 4c .. +3] =
+  // epilogue( sum_s W[s][m][...] ), 16 x 32 float4 over 256 threads
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = v[r] < thr ? thr : v[r];
+  for (int q = 0; q < 2; ++q) {
+    const int idx = tid + 256 * q;
+    const int m = idx >> 5;
+    const int n = n0 + 4 * (idx & 31);
+    if (m < args.M) {
+      f32x4 v = splitk_sum4(args.W + (size_t)m * args.ldw + n, (size_t)16 * args.ldw, splits);
+      if (args.bias) v += *(const f32x4*)(args.bias + n);
+      if (args.relu) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = v[r] < args.relu_threshold ? args.relu_threshold : v[r];
+      }
+      *(f32x4*)(args.C + (size_t)m * args.ldc + n) = v;
+    }
   }
-  *(f32x4*)(C + (size_t)m * ldc + n) = v;
+  splitk_release(args.counters + nb);
 }
 
 }  // namespace xtc_hip

@@ -48,6 +48,8 @@ struct DeviceState {
   hipStream_t stream = nullptr;
   void* workspace = nullptr;   // split-K partial sums
   size_t workspace_bytes = 0;
+  unsigned* counters = nullptr;  // split-K arrival counters (zero between launches)
+  size_t counters_len = 0;
   std::string arch, name;
 };
 
@@ -80,7 +82,8 @@ void* workspace(size_t bytes) {
   std::lock_guard<std::mutex> lk(g_mutex);
   if (d->workspace_bytes < bytes) {
     if (d->workspace) {
-      hipStreamSynchronize(d->stream);
+      // launches on any stream (callers may pass their own) may still read it
+      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
       hipFree(d->workspace);
       d->workspace = nullptr;
       d->workspace_bytes = 0;
@@ -89,6 +92,34 @@ void* workspace(size_t bytes) {
     d->workspace_bytes = bytes;
   }
   return d->workspace;
+}
+
+// Grows the per-device split-K arrival counters (splitk.hpp) to at least n
+// entries.  New counters are cleared here, once; every split-K launch leaves
+// them at zero.  Returns null on failure.
+unsigned* split_counters(size_t n) {
+  DeviceState* d = current_state();
+  if (!d) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mutex);
+  if (d->counters_len < n) {
+    const size_t len = n < 4096 ? 4096 : n;
+    if (d->counters) {
+      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+      hipFree(d->counters);
+      d->counters = nullptr;
+      d->counters_len = 0;
+    }
+    unsigned* p = nullptr;
+    if (hipMalloc((void**)&p, len * sizeof(unsigned)) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, len * sizeof(unsigned), d->stream) != hipSuccess ||
+        hipStreamSynchronize(d->stream) != hipSuccess) {
+      hipFree(p);
+      return nullptr;
+    }
+    d->counters = p;
+    d->counters_len = len;
+  }
+  return d->counters;
 }
 
 // ------------------------------------------------------------ aux kernels
@@ -168,24 +199,6 @@ __global__ void cast_bf16_f32_kernel(const uint16_t* x, float* y, uint64_t n) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) y[i] = __uint_as_float(((unsigned)x[i]) << 16);
-}
-
-// out[m][n] = epilogue( sum_s partial[s][m][n] ), summed in split order.
-__global__ void splitk_reduce_kernel(const float* __restrict__ partial, float* __restrict__ C,
-                                     const float* __restrict__ bias, int M, int N, int ldc,
-                                     int splits, int relu, float thr) {
-  uint64_t total = (uint64_t)M * N;
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (; i < total; i += stride) {
-    int m = (int)(i / N);
-    int n = (int)(i % N);
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += partial[(uint64_t)s * total + i];
-    if (bias) v += bias[n];
-    if (relu && v < thr) v = thr;
-    C[(uint64_t)m * ldc + n] = v;
-  }
 }
 
 template <typename T>
@@ -344,21 +357,17 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
   int splits = (a.K + kps - 1) / kps;
   a.k_per_split = kps;
   a.partial = nullptr;
+  a.counters = nullptr;
   if (splits > 1) {
     size_t bytes = (size_t)splits * a.M * a.N * sizeof(float);
     a.partial = (float*)workspace(bytes);
     if (!a.partial) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
+    a.counters = split_counters((size_t)a.tiles_m * a.tiles_n);
+    if (!a.counters) return fail("cannot allocate %d split-K counters", a.tiles_m * a.tiles_n);
   }
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
   e->launch(a, grid, s);
   HIP_TRY(hipGetLastError());
-  if (splits > 1) {
-    uint64_t total = (uint64_t)a.M * a.N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s,
-                       a.partial, a.C, a.bias, a.M, a.N, a.ldc, splits, a.relu,
-                       a.relu_threshold);
-    HIP_TRY(hipGetLastError());
-  }
   return 0;
 }
 
@@ -422,6 +431,9 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
   a.nblocks = d.N / 128;
   a.relu = d.relu;
   a.relu_threshold = d.relu_threshold;
+  a.C = C;
+  a.ldc = ldc;
+  a.counters = nullptr;
   if (splits == 1) {
     a.W = C;
     a.ldw = ldc;
@@ -430,6 +442,8 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
     a.W = (float*)workspace(bytes);
     if (!a.W) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
     a.ldw = d.N;
+    a.counters = split_counters((size_t)a.nblocks);
+    if (!a.counters) return fail("cannot allocate %d split-K counters", a.nblocks);
   }
   dim3 grid((unsigned)(a.nblocks * splits));
   if (d.K / splits == 1024)
@@ -437,12 +451,6 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
   else
     hipLaunchKernelGGL((gemm_bf16_skinny<512, 3>), grid, dim3(256), 0, s, a);
   HIP_TRY(hipGetLastError());
-  if (splits > 1) {
-    const int threads = d.M * (d.N / 4);
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a.W, C, bias,
-                       d.M, d.N, ldc, splits, d.relu, d.relu_threshold);
-    HIP_TRY(hipGetLastError());
-  }
   return 0;
 }
 

@@ -1,0 +1,151 @@
+// SPDX-License-Identifier: BSD-3-Clause
+// Split-K completion inside the GEMM launch: the workgroup that stores the
+// last partial tile of an output tile sums all of them, so a split-K GEMM
+// is one kernel (no second reduce launch, no launch gap).
+//
+// Protocol, per output tile with `splits` workgroups along K:
+//   1. every workgroup stores its fp32 partial tile to the workspace with
+//      agent-scope atomic stores (gfx950: global_store ... sc1, written
+//      through to the device coherence point, so the other XCDs' L2s never
+//      hold it dirty);
+//   2. every thread waits for its stores to complete (vmcnt(0)), the
+//      workgroup synchronises and one lane increments the tile's arrival
+//      counter (agent-scope atomic add);
+//   3. the workgroup that sees splits-1 is the last one: it reads the
+//      partials back with agent-scope atomic loads (global_load ... sc1),
+//      sums partial[0..splits-1] in split order (the result does not depend
+//      on which workgroup arrived last), applies bias / relu, stores C and
+//      sets the counter back to 0 for the next launch.
+// Every access to the published data is itself an agent-scope atomic, so no
+// L2 write-back (buffer_wbl2) or invalidate (buffer_inv) is needed: a
+// release/acquire fence at agent scope would write back and invalidate the
+// whole L2 of the XCD in every workgroup, which costs more than the reduce.
+// Counters start at zero (the host clears them once when it allocates them)
+// and every launch leaves them at zero.  Two launches that share the
+// counters and the workspace must not overlap (one stream per device).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xtc_hip {
+
+namespace splitk {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maximum (no wait)
+constexpr int kWaitVm0 = (7 << 4) | (15 << 8);
+}  // namespace splitk
+
+__device__ __forceinline__ void splitk_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float splitk_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte aligned p: two 8-byte agent-scope stores / loads.
+__device__ __forceinline__ void splitk_store4(float* p, splitk::f32x4 v) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(p);
+  const uint64_t lo = (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32);
+  const uint64_t hi = (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32);
+  __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ splitk::f32x4 splitk_load4(const float* p) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
+  const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return splitk::f32x4{__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
+                       __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32))};
+}
+
+// sum_{s < splits} p[s * stride] in split order, 8 loads in flight.  A slot
+// past the last split adds +0.0, which leaves the sum unchanged: it starts at
+// +0.0 and so is never -0.0.
+__device__ __forceinline__ splitk::f32x4 splitk_sum4(const float* p, size_t stride, int splits) {
+  constexpr int kBatch = 8;
+  splitk::f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += kBatch) {
+    splitk::f32x4 t[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) t[j] = splitk_load4(p + (size_t)min(s0 + j, splits - 1) * stride);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) v += s0 + j < splits ? t[j] : splitk::f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  return v;
+}
+
+__device__ __forceinline__ float splitk_sum1(const float* p, size_t stride, int splits) {
+  constexpr int kBatch = 8;
+  float v = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += kBatch) {
+    float t[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) t[j] = splitk_load(p + (size_t)min(s0 + j, splits - 1) * stride);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) v += s0 + j < splits ? t[j] : 0.f;
+  }
+  return v;
+}
+
+// Step 2: true in the last-arriving workgroup only.  Called by every thread
+// of the workgroup (1-D blocks) after its splitk_store calls.
+__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int splits) {
+  __shared__ unsigned s_last;
+  __builtin_amdgcn_s_waitcnt(splitk::kWaitVm0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(splits - 1)
+                 ? 1u
+                 : 0u;
+  __syncthreads();
+  return s_last != 0;
+}
+
+// Ends the protocol in the last workgroup (after its reads of the partials).
+__device__ __forceinline__ void splitk_release(unsigned* counter) {
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The last workgroup's sum over one BM x BN output tile at (m0, n0):
+// C[m][n] = epilogue( sum_s partial[s][m][n] ), partial is [splits][M][N].
+// Four columns per thread when N, ldc and the pointers allow it; the sums
+// are the same element by element either way.
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void splitk_finish_tile(const float* partial, float* C, const float* bias, int M,
+                                                   int N, int ldc, int splits, int relu, float thr, int m0,
+                                                   int n0) {
+  using splitk::f32x4;
+  const size_t plane = (size_t)M * N;
+  const int tid = threadIdx.x;
+  const bool vec = BN % 4 == 0 && ((N | ldc) & 3) == 0 && (((uintptr_t)C | (uintptr_t)partial) & 15) == 0 &&
+                   (bias == nullptr || ((uintptr_t)bias & 15) == 0);
+  if (vec) {
+    for (int idx = tid; idx < BM * BN / 4; idx += NT) {
+      const int m = m0 + idx / (BN / 4);
+      const int n = n0 + 4 * (idx % (BN / 4));
+      if (m >= M || n >= N) continue;
+      f32x4 v = splitk_sum4(partial + (size_t)m * N + n, plane, splits);
+      if (bias) v += *(const f32x4*)(bias + n);
+      if (relu) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = v[r] < thr ? thr : v[r];
+      }
+      *(f32x4*)(C + (size_t)m * ldc + n) = v;
+    }
+  } else {
+    for (int idx = tid; idx < BM * BN; idx += NT) {
+      const int m = m0 + idx / BN;
+      const int n = n0 + idx % BN;
+      if (m >= M || n >= N) continue;
+      float v = splitk_sum1(partial + (size_t)m * N + n, plane, splits);
+      if (bias) v += bias[n];
+      if (relu && v < thr) v = thr;
+      C[(size_t)m * ldc + n] = v;
+    }
+  }
+}
+
+}  // namespace xtc_hip
