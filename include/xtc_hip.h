@@ -94,24 +94,31 @@ typedef struct {
   int bm, bn, bk, wgm, wgn;
 } xtc_hip_tile;
 
-/* C[M,N] = relu?( A[M,K] @ B[K,N] + bias[N]? ), fp32 output.
+/* C[M,N] = relu?( op(A)[M,K] @ op(B)[K,N] + bias[N]? ), fp32 output.
  * Replaces the scheduled linalg.fill + linalg.matmul pair of
  * MlirOperatorMatmul.generate_op (src/xtc/backends/mlir/MlirOps.py:189-270),
  * with XTCOperMatmul semantics (src/xtc/graphs/xtc/operators.py:159-221):
  * A is the input viewed as (shape[0], prod(rest)), B as (prod(rest[:-1]),
  * last).  The relu node of XTCOperRelu (operators.py:224-249) may be fused
- * as the epilogue: out = max(out, relu_threshold), NaN preserved. */
+ * as the epilogue: out = max(out, relu_threshold), NaN preserved.
+ * trans_a / trans_b are the operand layouts of XTC tensor types: layout
+ * [1, 0] stores the operand transposed (MlirOperatorMatmul.args_from_operation
+ * and its transposed indexing maps, MlirOps.py:171-178,213-254; NDArray's
+ * transposed storage, src/xtc/runtimes/types/ndarray.py:70-102).  With
+ * trans_a, A is read from At[K][lda >= M]; with trans_b, B from Bt[N][ldb >= K]. */
 typedef struct {
   int dtype;             /* xtc_hip_dtype of A and B; C is always fp32 */
   int M, N, K;
-  int lda, ldb, ldc;     /* row strides in elements, 0 = dense */
+  int lda, ldb, ldc;     /* row strides in elements of the stored matrices, 0 = dense */
   xtc_hip_tile tile;
-  int split_k;           /* >= 1: K partitions reduced by a second kernel */
+  int split_k;           /* >= 1: K partitions, summed inside the launch */
   int group_m;           /* raster group height in tiles, 0 = default */
   int xcd_remap;         /* 1 = map consecutive tiles onto one XCD */
   int relu;
   float relu_threshold;
   void *stream;          /* hipStream_t, NULL = library stream */
+  int trans_a;           /* 1: A stored transposed, [K][lda] */
+  int trans_b;           /* 1: B stored transposed, [N][ldb] */
 } xtc_hip_matmul_desc;
 
 int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B,

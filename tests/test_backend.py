@@ -139,6 +139,76 @@ def test_unsupported_operator_and_dtype_raise():
         Backend(_matmul(16, 16, 16, "float64"))
 
 
+def test_operand_layouts_lower_to_transpose_flags(tmp_path):
+    # layout [1, 0] on matmul operands, as tests/filecheck/backends/test_matmul_mlir_layout.py
+    a = O.tensor((4, 512), "float32", name="A", layout=[1, 0])
+    b = O.tensor((512, 32), "float32", name="B", layout=[1, 0])
+    with O.graph(name="matmul_layout") as gb:
+        O.matmul(a, b, name="C")
+    assert "4x512xfloat32, <(0,1)->(1,0)>" in str(gb.graph)
+    backend = Backend(gb.graph)
+    (ln,) = backend.plan.launches
+    assert ln.attrs["trans_a"] and ln.attrs["trans_b"] and (ln.attrs["M"], ln.attrs["N"], ln.attrs["K"]) == (4, 32, 512)
+    module = backend.get_compiler(dump_file=str(tmp_path / "ml")).compile(backend.get_scheduler().schedule())
+    # the two flags close the descriptor initializer (fields trans_a, trans_b)
+    assert re.search(r"xtc_hip_matmul_desc d = \{.*, 1, 1\};", module.source)
+    natural = Backend(_matmul(4, 32, 512)).plan.launches[0].attrs
+    assert not natural["trans_a"] and not natural["trans_b"]
+
+
+def test_layouts_outside_matmul_operands_raise():
+    # the reference's MLIR backend raises for them too (MlirOps.py:45-52,
+    # tests/filecheck/backends/invalid/test_relu_mlir_layout.py)
+    a = O.tensor((4, 32), "float32", name="A", layout=[1, 0])
+    with O.graph(name="relu_layout") as gb:
+        O.relu(a, name="relu")
+    with pytest.raises(UnsupportedGraph, match="layout"):
+        Backend(gb.graph)
+    x = O.tensor((64, 16), "float32", name="X")
+    w = O.tensor((16, 8), "float32", name="W")
+    bias = O.tensor((8, 1), "float32", name="b", layout=[1, 0])
+    with O.graph(name="bias_layout") as gb:
+        O.bias_add(O.matmul(x, w, name="mm"), O.reshape(bias, (8,)), name="ba")
+    with pytest.raises(UnsupportedGraph, match="layout"):
+        Backend(gb.graph)
+
+
+def test_device_array_layout_round_trip_on_host(monkeypatch):
+    # DeviceArray with layout [1, 0] stores the transpose and hands back the
+    # logical array; a fake device (host memory) checks the byte order.
+    from xtc_amd.runtimes.hip.ndarray import DeviceArray
+
+    class FakeDevice:
+        def __init__(self):
+            self.mem = {}
+
+        def memory_allocate(self, n):
+            buf = (ctypes.c_char * n)()
+            self.mem[ctypes.addressof(buf)] = buf
+            return ctypes.addressof(buf)
+
+        def memory_copy_to(self, dst, src, n):
+            ctypes.memmove(dst, src, n)
+
+        def memory_copy_from(self, src, dst, n):
+            ctypes.memmove(dst, src, n)
+
+        def memory_free(self, h):
+            self.mem.pop(h, None)
+
+    import numpy as np
+
+    dev = FakeDevice()
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    d = DeviceArray.from_numpy(x, "float32", dev, [1, 0])
+    stored = np.frombuffer(dev.mem[d.data], dtype=np.float32).reshape(4, 3)
+    np.testing.assert_array_equal(stored, x.T)
+    np.testing.assert_array_equal(d.numpy(), x)
+    assert DeviceArray.from_numpy(x, "float32", dev, [0, 1]).layout is None
+    with pytest.raises(ValueError):
+        DeviceArray((2, 3, 4), "float32", dev, [2, 1, 0])
+
+
 # ---------------------------------------------------------------- scheduler
 
 def test_default_node_writes_the_output():

@@ -340,6 +340,77 @@ def _run_strided(a, b, tile, lda, ldb, ldc, relu=False, bias=None, split_k=1):
     return C.to_numpy((M, ldc), np.float32)[:, :N]
 
 
+def run_matmul_layout(a, b, dtype, ta, tb, tile=None, split_k=0, pad_a=0, pad_b=0, relu=False, bias=None):
+    """C = a @ b with A stored transposed (At[K][M + pad_a]) when ta and B
+    stored transposed (Bt[N][K + pad_b]) when tb, else row-major with the
+    same padding of the leading dimension."""
+    M, K = a.shape
+    N = b.shape[1]
+    sa = a.T if ta else a
+    sb = b.T if tb else b
+    ap = np.zeros((sa.shape[0], sa.shape[1] + pad_a), np.float32)
+    ap[:, : sa.shape[1]] = sa
+    bp = np.zeros((sb.shape[0], sb.shape[1] + pad_b), np.float32)
+    bp[:, : sb.shape[1]] = sb
+    A, B = _dev(ap, dtype), _dev(bp, dtype)
+    C = DeviceBuffer(M * N * 4)
+    bias_buf = DeviceBuffer.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    d = capi.MatmulDesc()
+    d.dtype = capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb = ap.shape[1], bp.shape[1]
+    d.trans_a, d.trans_b = int(ta), int(tb)
+    if tile is not None:
+        d.tile = capi.Tile(*tile)
+    d.split_k = split_k
+    d.xcd_remap = 1
+    d.relu = int(relu)
+    L = capi.lib()
+    capi.check(L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, bias_buf.c_ptr if bias_buf else None),
+               "matmul")
+    capi.check(L.xtc_hip_synchronize(), "sync")
+    return C.to_numpy((M, N), np.float32)
+
+
+LAYOUTS = [(True, False), (False, True), (True, True)]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_matmul_operand_layouts_integer_exact(dtype, ta, tb):
+    # transposed storage (tensor layout [1, 0]) on every kernel family: the
+    # generic template (ragged and aligned shapes, split-K), the skinny bf16
+    # kernel and the LDS-DMA kernel (B^T read natively, A^T via a transposed
+    # copy); padded leading dimensions on the stored matrices
+    cases = [((64, 96, 128), None, 0, 0, 0), ((70, 130, 200), None, 0, 8, 4), ((96, 160, 2048), None, 4, 0, 0)]
+    if dtype == "bfloat16":
+        cases += [((256, 512, 256), (256, 256, 64, 2, 4), 0, 0, 0), ((512, 256, 320), (256, 256, 64, 4, 2), 0, 16, 8),
+                  ((16, 1024, 8192), (16, 128, 64, 1, 4), 8, 0, 0)]
+    for (M, N, K), tile, split, pad_a, pad_b in cases:
+        a, b = _int_operands(M, N, K, 5)
+        out = run_matmul_layout(a, b, dtype, ta, tb, tile=tile, split_k=split, pad_a=pad_a, pad_b=pad_b)
+        np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32),
+                                      err_msg=f"{dtype} ta={ta} tb={tb} {(M, N, K)} tile={tile}")
+
+
+@pytest.mark.parametrize("waves", [(2, 4), (4, 2)])
+def test_lds_dma_bf16_transposed_b_seeded_bias_relu(waves):
+    # B^T feeds the LDS-DMA kernel directly; seeded inputs, padded strides
+    rng = np.random.default_rng(41)
+    M, N, K = 512, 768, 1024
+    a = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    out = run_matmul_layout(a, b, "bfloat16", False, True, tile=(256, 256, 64, *waves), pad_a=8, pad_b=64,
+                            relu=True, bias=bias)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_BF16
+    # and bit-identical to the row-major B path: same fragments, same order
+    same = run_matmul_layout(a, b, "bfloat16", False, False, tile=(256, 256, 64, *waves), pad_a=8, pad_b=64,
+                             relu=True, bias=bias)
+    np.testing.assert_array_equal(out, same)
+
+
 @pytest.mark.parametrize("waves", [(2, 4), (4, 2)])
 def test_lds_dma_bf16_integer_exact(waves):
     M, N, K = 512, 768, 1024

@@ -239,3 +239,36 @@ def test_validation_failure_is_reported():
     bad = lambda *args: [np.copyto(o, 0) for o in args[2:]]  # noqa: E731
     res, code, msg = module.get_evaluator(validate=True, reference_impl=bad, min_repeat_ms=0).evaluate()
     assert code == 1 and "validation" in msg
+
+
+def _layout_graph(m, n, k, dtype, la, lb, name):
+    a = O.tensor((m, k), dtype, name="A", layout=[1, 0] if la else None)
+    b = O.tensor((k, n), dtype, name="B", layout=[1, 0] if lb else None)
+    with O.graph(name=name) as gb:
+        O.matmul(a, b, name="C", **({"out_dtype": "float32"} if dtype == "bfloat16" else {}))
+    return gb.graph
+
+
+@pytest.mark.parametrize("la,lb", [(True, False), (False, True), (True, True)])
+def test_operand_layouts_validate(la, lb):
+    # tests/filecheck/backends/test_matmul_mlir_layout.py: A (4x512) with
+    # layout [1, 0], executed with validate=True -> CODE: 0
+    module = _compile(_layout_graph(4, 32, 512, "float32", la, lb, "matmul_layout"))
+    assert module.get_executor(validate=True).execute() == 0
+    # the bf16 C3a kernel family with B^T read natively (and A^T staged)
+    module = _compile(_layout_graph(512, 512, 512, "bfloat16", la, lb, "matmul_layout_bf16"),
+                      tiles={"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 64}})
+    res, code, msg = module.get_evaluator(validate=True, repeat=1, number=1, min_repeat_ms=0).evaluate()
+    assert code == 0, msg
+
+
+def test_operand_layouts_seeded_logical_parameters():
+    # parameters are logical arrays; the evaluator stores [1, 0] inputs
+    # transposed on the device, like the reference's NDArray
+    rng = np.random.default_rng(7)
+    a = ref.round_bf16(rng.uniform(-1, 1, (256, 1024)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (1024, 768)).astype(np.float32))
+    module = _compile(_layout_graph(256, 768, 1024, "bfloat16", False, True, "nt_seeded"),
+                      tiles={"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 64}})
+    (out,) = _run(module, [a, b])
+    assert ref.scaled_error(out, ref.matmul(a, b), 1024, 1.0, 1.0) <= TOL_BF16

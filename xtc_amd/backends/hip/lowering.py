@@ -10,7 +10,8 @@ HBM):
   * bias_add on a matmul/conv2d result -> GEMM epilogue;
   * relu on a matmul/conv2d(/bias_add) result -> GEMM epilogue.
 A fusion happens only when the intermediate is used once and is not a graph
-output.  reshape is a view.  The reference lowers each node to its own
+output.  A matmul operand with layout [1, 0] (stored transposed) becomes the
+launch's trans_a / trans_b flag; other operators require natural layouts.  reshape is a view.  The reference lowers each node to its own
 linalg op (src/xtc/backends/mlir/MlirOps.py:166-782) and fuses only through
 transform-dialect producer fusion (MlirCompilerPasses.py:378-412).
 
@@ -184,7 +185,28 @@ def lower_graph(graph: Any) -> Plan:
             pad_fusion[n.uid] = (pad_node, hw)
             absorbed.add(pad_node.uid)
 
+    def transposed_inputs(n: Any) -> tuple[bool, ...]:
+        """Per input: stored transposed (layout [1, 0]).  Only the two 2-D
+        operands of a matmul may be (MlirOps.py:171-178); other operators
+        need natural layouts, as in the reference (MlirOps.py:45-52)."""
+        flags = []
+        for idx, u in enumerate(n.inputs):
+            t = out_type(u)
+            lay = getattr(t, "layout", None)
+            shp = _shape(t)
+            if lay is None or list(lay) == list(range(len(shp))):
+                flags.append(False)
+            elif n.operation.name == "matmul" and idx < 2 and len(shp) == 2 and list(lay) == [1, 0]:
+                flags.append(True)
+            else:
+                raise UnsupportedGraph(
+                    f"{n.operation.name} {n.name}: tensor layout {list(lay)} of input {idx} is not supported "
+                    "(only [1, 0] on a 2-D matmul operand)"
+                )
+        return tuple(flags)
+
     for n in order:
+        trans = transposed_inputs(n)  # also checks the nodes a kernel absorbs
         if n.uid in absorbed:
             continue
         op = n.operation
@@ -201,7 +223,7 @@ def lower_graph(graph: Any) -> Plan:
             src_inputs = list(n.inputs)
             if name == "matmul":
                 i, j, k = (int(op.dims[d]) for d in ("i", "j", "k"))
-                attrs.update(M=i, N=j, K=k)
+                attrs.update(M=i, N=j, K=k, trans_a=trans[0], trans_b=trans[1])
             else:
                 pads = (0, 0, 0, 0)
                 pad_value = 0.0

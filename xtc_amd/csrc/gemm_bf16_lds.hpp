@@ -1,7 +1,9 @@
 // SPDX-License-Identifier: BSD-3-Clause
 // bf16 GEMM for aligned large shapes on gfx950 (CDNA4):
-//   C[M,N] (fp32) = epilogue( A[M,K] (bf16, row-major) @ B[K,N] (bf16, row-major) )
+//   C[M,N] (fp32) = epilogue( A[M,K] (bf16, row-major) @ B[K,N] (bf16) )
 // with M % 256 == 0, N % 256 == 0, K % BK == 0 and 16-byte aligned rows.
+// B is row-major [K][ldb] (BT = false) or stored transposed, [N][ldb] with
+// k contiguous (BT = true: the tensor layout [1, 0]).
 //
 // Design (one 256x256 output tile per workgroup, WGM x WGN waves):
 //   * K is walked in BK-deep slabs through STAGES LDS stages (distinct LDS
@@ -21,7 +23,10 @@
 //     128-byte rows (BK=64) and by (r >> 1) & 3 for 64-byte rows (BK=32): the
 //     best patterns measured for this access on MI355X (174 and 218 B/clk/CU;
 //     contiguous b128 reads give 191).
-//   * B stays row-major in LDS (BK k-rows x 512 B) and is read transposed by
+//   * BT: B's stage has A's shape (256 n-rows x 2*BK bytes), is filled,
+//     swizzled and read exactly like A (ds_read_b128), and B fragment jt of
+//     a lane is the A-style fragment of n-row col0 + jt*16 + l16.
+//   * !BT: B stays row-major in LDS (BK k-rows x 512 B) and is read transposed by
 //     ds_read_b64_tr_b16: within a 16-lane group, output lane i element q is
 //     element (i % 4) of the 8 bytes addressed by lane 4q + i/4, so lane j
 //     addresses B[k0 + j/4][n0 + 4(j%4) .. +3] to receive B[k0 .. k0+3][n0+j].
@@ -102,7 +107,9 @@ struct Frags {
 // Reads k-step `ks` of a stage (A at `sa`, B at `sb`).
 //   A fragment `it`: lane (l16, g) gets A[row0 + it*16 + l16][ks*32 + 8g .. +7]
 //   B fragment `jt`: lane (l16, g) gets B[ks*32 + 8g .. +7][col0 + jt*16 + l16]
-template <int BK, int TM, int TN>
+// With BT the B coordinates are those of an A-style operand: b_krow0 is the
+// lane's first n-row (wn*16*TN + l16) and b_f its chunk swizzle; b_c0 unused.
+template <int BK, bool BT, int TM, int TN>
 __device__ __forceinline__ void read_frags(Frags<TM, TN>& f, const unsigned char* sa, const unsigned char* sb, int ks,
                                            int a_row0, int a_h, int g, int b_krow0, int b_f, int b_c0, int l16) {
 #pragma unroll
@@ -112,15 +119,21 @@ __device__ __forceinline__ void read_frags(Frags<TM, TN>& f, const unsigned char
   }
 #pragma unroll
   for (int jt = 0; jt < TN; ++jt) {
-    const int c32 = (b_c0 + jt) ^ b_f;
-    const int off0 = (ks * 32 + b_krow0) * 512 + c32 * 32 + 8 * (l16 & 3);
-    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
-    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
-    f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    if constexpr (BT) {
+      const int off = (b_krow0 + jt * 16) * (2 * BK) + 16 * ((ks * 4 + g) ^ b_f);
+      f.b[jt] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sb + off));
+    } else {
+      const int c32 = (b_c0 + jt) ^ b_f;
+      const int off0 = (ks * 32 + b_krow0) * 512 + c32 * 32 + 8 * (l16 & 3);
+      i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
+      i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
+      f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
   }
 }
 
-// One A fragment (one ds_read_b128) / one B fragment (two ds_read_b64_tr_b16)
+// One A fragment (one ds_read_b128) / one B fragment (two ds_read_b64_tr_b16,
+// or one ds_read_b128 with BT)
 // of k-step ks, with the same addressing as read_frags.
 template <int BK, int TM, int TN>
 __device__ __forceinline__ void read_a1(Frags<TM, TN>& f, const unsigned char* sa, int ks, int it, int a_row0, int a_h,
@@ -128,14 +141,19 @@ __device__ __forceinline__ void read_a1(Frags<TM, TN>& f, const unsigned char* s
   const int off = (a_row0 + it * 16) * (2 * BK) + 16 * ((ks * 4 + g) ^ a_h);
   f.a[it] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sa + off));
 }
-template <int TM, int TN>
+template <int BK, bool BT, int TM, int TN>
 __device__ __forceinline__ void read_b1(Frags<TM, TN>& f, const unsigned char* sb, int ks, int jt, int b_krow0, int b_f,
-                                        int b_c0, int l16) {
-  const int c32 = (b_c0 + jt) ^ b_f;
-  const int off0 = (ks * 32 + b_krow0) * 512 + c32 * 32 + 8 * (l16 & 3);
-  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
-  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
-  f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                                        int b_c0, int l16, int g) {
+  if constexpr (BT) {
+    const int off = (b_krow0 + jt * 16) * (2 * BK) + 16 * ((ks * 4 + g) ^ b_f);
+    f.b[jt] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sb + off));
+  } else {
+    const int c32 = (b_c0 + jt) ^ b_f;
+    const int off0 = (ks * 32 + b_krow0) * 512 + c32 * 32 + 8 * (l16 & 3);
+    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0));
+    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + off0 + 4 * 512));
+    f.b[jt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
 }
 
 // The two k-steps of a 64-deep slab in a fixed order (sched_barrier fences
@@ -147,7 +165,7 @@ __device__ __forceinline__ void read_b1(Frags<TM, TN>& f, const unsigned char* s
 // bit-identical to it.  Left to itself the scheduler issues all 40 reads
 // first and waits for every one of them before the first MFMA (an LDS DMA
 // in flight makes the compiler's LDS waits all-or-nothing).
-template <int BK, int TM, int TN>
+template <int BK, bool BT, int TM, int TN>
 __device__ __forceinline__ void slab64(f32x4 (&acc)[TM][TN], const unsigned char* sa, const unsigned char* sb,
                                        int a_row0, int a_h, int g, int b_krow0, int b_f, int b_c0, int l16) {
   constexpr int LA = 2;
@@ -156,15 +174,15 @@ __device__ __forceinline__ void slab64(f32x4 (&acc)[TM][TN], const unsigned char
 #pragma unroll
   for (int it = 0; it < TM; ++it) read_a1<BK>(f0, sa, 0, it, a_row0, a_h, g);
 #pragma unroll
-  for (int jt = 0; jt < LA && jt < TN; ++jt) read_b1(f0, sb, 0, jt, b_krow0, b_f, b_c0, l16);
+  for (int jt = 0; jt < LA && jt < TN; ++jt) read_b1<BK, BT>(f0, sb, 0, jt, b_krow0, b_f, b_c0, l16, g);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int jt = 0; jt < TN; ++jt) {
-    if (jt + LA < TN) read_b1(f0, sb, 0, jt + LA, b_krow0, b_f, b_c0, l16);
+    if (jt + LA < TN) read_b1<BK, BT>(f0, sb, 0, jt + LA, b_krow0, b_f, b_c0, l16, g);
 #pragma unroll
     for (int q = jt * NF1 / TN; q < (jt + 1) * NF1 / TN; ++q) {
       if (q < TM) read_a1<BK>(f1, sa, 1, q, a_row0, a_h, g);
-      else read_b1(f1, sb, 1, q - TM, b_krow0, b_f, b_c0, l16);
+      else read_b1<BK, BT>(f1, sb, 1, q - TM, b_krow0, b_f, b_c0, l16, g);
     }
 #pragma unroll
     for (int it = 0; it < TM; ++it)
@@ -190,7 +208,7 @@ __device__ __forceinline__ void mma(f32x4 (&acc)[TM][TN], const Frags<TM, TN>& f
 }  // namespace big
 
 // WGM x WGN waves; each wave owns a (256/WGM) x (256/WGN) sub-tile.
-template <int WGM, int WGN, int BK, int STAGES>
+template <int WGM, int WGN, int BK, int STAGES, bool BT = false>
 __global__ void __attribute__((amdgpu_flat_work_group_size(WGM * WGN * 64, WGM * WGN * 64)))
 gemm_bf16_256x256(BigGemmArgs args) {
   using namespace big;
@@ -236,13 +254,17 @@ gemm_bf16_256x256(BigGemmArgs args) {
     const int kb = wave * KB_PER_WAVE + i;
     const int arow = kb * A_ROWS_PER_KB + lane / A_CHUNKS;
     a_off[i] = arow * args.lda + ((lane % A_CHUNKS) ^ swz_a<BK>(arow)) * 8;
-    const int bk = kb * 2 + (lane >> 5);  // B: 2 k-rows of 512 B per KB
-    const int slot = lane & 31;
-    b_off[i] = bk * args.ldb + ((slot >> 1) ^ swz_b(bk)) * 16 + (slot & 1) * 8;
+    if constexpr (BT) {  // B^T rows like A rows
+      b_off[i] = arow * args.ldb + ((lane % A_CHUNKS) ^ swz_a<BK>(arow)) * 8;
+    } else {
+      const int bk = kb * 2 + (lane >> 5);  // B: 2 k-rows of 512 B per KB
+      const int slot = lane & 31;
+      b_off[i] = bk * args.ldb + ((slot >> 1) ^ swz_b(bk)) * 16 + (slot & 1) * 8;
+    }
   }
   const __bf16* a_base = args.A + (size_t)m0 * args.lda;
-  const __bf16* b_base = args.B + n0;
-  const size_t b_step = (size_t)BK * args.ldb;
+  const __bf16* b_base = BT ? args.B + (size_t)n0 * args.ldb : args.B + n0;
+  const size_t b_step = BT ? (size_t)BK : (size_t)BK * args.ldb;
   const int nk = args.K / BK;
   // K-stagger: tile (tm, tn) walks K starting at slab (tm + 2 tn) mod 16, so
   // the tiles sharing an A panel (same tm) or a B panel (same tn) do not
@@ -272,9 +294,11 @@ gemm_bf16_256x256(BigGemmArgs args) {
   const int g = lane >> 4;
   const int a_row0 = wm * (16 * TM) + l16;
   const int a_h = swz_a<BK>(a_row0);    // depends on l16 only
-  const int b_krow0 = 8 * g + (l16 >> 2);
-  const int b_f = swz_b(b_krow0);       // unchanged by ks*32 and the +4 half
-  const int b_c0 = wn * TN;             // first 32-byte chunk of the wave's columns
+  // !BT: first k-row of the lane's transposed reads and its chunk swizzle
+  // (unchanged by ks*32 and the +4 half).  BT: first n-row and its swizzle.
+  const int b_krow0 = BT ? wn * (16 * TN) + l16 : 8 * g + (l16 >> 2);
+  const int b_f = BT ? swz_a<BK>(b_krow0) : swz_b(b_krow0);
+  const int b_c0 = wn * TN;             // !BT: first 32-byte chunk of the wave's columns
 
   f32x4 acc[TM][TN];
 #pragma unroll
@@ -296,12 +320,12 @@ gemm_bf16_256x256(BigGemmArgs args) {
     if (kt + STAGES - 1 < nk) issue_slab(kt + STAGES - 1, stages[(s + STAGES - 1) % STAGES]);
     const unsigned char* sa = stages[s];
     if constexpr (BK == 64) {
-      slab64<BK>(acc, sa, sa + A_STAGE, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
+      slab64<BK, BT>(acc, sa, sa + A_STAGE, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
     } else {
 #pragma unroll
       for (int ks = 0; ks < BK / 32; ++ks) {
         Frags<TM, TN> f;
-        read_frags<BK>(f, sa, sa + A_STAGE, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
+        read_frags<BK, BT>(f, sa, sa + A_STAGE, ks, a_row0, a_h, g, b_krow0, b_f, b_c0, l16);
         mma(acc, f);
       }
     }

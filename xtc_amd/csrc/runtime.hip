@@ -50,6 +50,8 @@ struct DeviceState {
   size_t workspace_bytes = 0;
   unsigned* counters = nullptr;  // split-K arrival counters (zero between launches)
   size_t counters_len = 0;
+  void* staging[2] = {nullptr, nullptr};  // natural copies of transposed operands
+  size_t staging_bytes[2] = {0, 0};
   std::string arch, name;
 };
 
@@ -92,6 +94,25 @@ void* workspace(size_t bytes) {
     d->workspace_bytes = bytes;
   }
   return d->workspace;
+}
+
+// Grows staging buffer `slot` (0: A, 1: B) of the current device.  Returns
+// null on failure.
+void* staging(int slot, size_t bytes) {
+  DeviceState* d = current_state();
+  if (!d) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mutex);
+  if (d->staging_bytes[slot] < bytes) {
+    if (d->staging[slot]) {
+      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+      hipFree(d->staging[slot]);
+      d->staging[slot] = nullptr;
+      d->staging_bytes[slot] = 0;
+    }
+    if (hipMalloc(&d->staging[slot], bytes) != hipSuccess) return nullptr;
+    d->staging_bytes[slot] = bytes;
+  }
+  return d->staging[slot];
 }
 
 // Grows the per-device split-K arrival counters (splitk.hpp) to at least n
@@ -374,11 +395,12 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // The LDS-DMA bf16 kernel (gemm_bf16_lds.hpp) implements the 256x256x64
-// tiles with 2x4 and 4x2 waves when the shape needs no bounds checks.
+// tiles with 2x4 and 4x2 waves when the shape needs no bounds checks, for B
+// row-major (bt = false, ldb >= N) or stored transposed (bt = true, ldb >= K).
 // XTC_HIP_GENERIC_GEMM=1 forces the generic template (for A/B comparisons).
 bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
                           int ldb, int ldc, const void* A, const void* B, const void* C,
-                          const void* bias) {
+                          const void* bias, bool bt) {
   static const bool disabled = [] {
     const char* v = getenv("XTC_HIP_GENERIC_GEMM");
     return v && v[0] == '1';
@@ -390,7 +412,7 @@ bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
   if (lda % 8 || ldb % 8 || ldc % 4) return false;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
   // element offsets of one tile row/column range must fit in 32 bits
-  if ((int64_t)256 * lda > INT32_MAX || (int64_t)64 * ldb > INT32_MAX) return false;
+  if ((int64_t)256 * lda > INT32_MAX || (int64_t)(bt ? 256 : 64) * ldb > INT32_MAX) return false;
   return true;
 }
 
@@ -507,7 +529,7 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, int OH, int OW, const void*
 
 int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int lda, int ldb,
                         int ldc, const void* A, const void* B, float* C, const float* bias,
-                        hipStream_t s) {
+                        hipStream_t s, bool bt) {
   BigGemmArgs a;
   a.A = (const __bf16*)A;
   a.B = (const __bf16*)B;
@@ -523,15 +545,71 @@ int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int
   a.relu_threshold = d.relu_threshold;
   a.tiles_m = d.M / 256;
   a.tiles_n = d.N / 256;
-  a.group_m = d.group_m > 0 ? d.group_m : 16;  // best measured at 8192^3
+  a.group_m = d.group_m > 0 ? d.group_m : 8;  // 8 <= 16 at 8192^3, zero and random data
   a.xcd_remap = d.xcd_remap;
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (t.wgm == 2)
-    hipLaunchKernelGGL((gemm_bf16_256x256<2, 4, 64, 2>), grid, dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((gemm_bf16_256x256<4, 2, 64, 2>), grid, dim3(512), 0, s, a);
+  if (t.wgm == 2) {
+    if (bt)
+      hipLaunchKernelGGL((gemm_bf16_256x256<2, 4, 64, 2, true>), grid, dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_bf16_256x256<2, 4, 64, 2, false>), grid, dim3(512), 0, s, a);
+  } else {
+    if (bt)
+      hipLaunchKernelGGL((gemm_bf16_256x256<4, 2, 64, 2, true>), grid, dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_bf16_256x256<4, 2, 64, 2, false>), grid, dim3(512), 0, s, a);
+  }
   HIP_TRY(hipGetLastError());
   return 0;
+}
+
+// dst[c][r] = src[r][c] for r < R, c < Cc; src rows ld_src apart, dst dense
+// [Cc][R].  64x64 tiles through LDS (padded row: the column reads hit 64
+// distinct banks), coalesced 64-element rows on both sides.  HBM-bound:
+// sizeof(T) bytes read + written per element.
+template <typename T>
+__global__ void __launch_bounds__(256) transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int R, int Cc,
+                                                        int ld_src) {
+  __shared__ T tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    if (r < R && c < Cc) tile[i][tx] = src[(size_t)r * ld_src + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = ty; i < 64; i += 4) {
+    const int c = c0 + i, r = r0 + tx;
+    if (c < Cc && r < R) dst[(size_t)c * R + r] = tile[tx][i];
+  }
+}
+
+// Dense [Cc][R] copy of the R x Cc matrix at src (row stride ld_src) in
+// staging buffer `slot`; null on failure (g_last_error set).
+const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src, int elem_bytes, hipStream_t s) {
+  const size_t bytes = (size_t)R * Cc * elem_bytes;
+  void* dst = staging(slot, bytes);
+  if (!dst) {
+    fail("cannot allocate %zu bytes of transpose staging", bytes);
+    return nullptr;
+  }
+  dim3 grid((unsigned)((Cc + 63) / 64), (unsigned)((R + 63) / 64));
+  if (grid.y > 65535u) {
+    fail("transpose: %d rows exceed the grid limit", R);
+    return nullptr;
+  }
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, s, (const float*)src, (float*)dst, R, Cc, ld_src);
+  else
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)src, (uint16_t*)dst, R,
+                       Cc, ld_src);
+  if (hipGetLastError() != hipSuccess) {
+    fail("transpose launch failed");
+    return nullptr;
+  }
+  return dst;
 }
 
 }  // namespace
@@ -709,11 +787,36 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
   const xtc_hip_matmul_desc& d = *desc;
   if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
   if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
-  const int lda = d.lda ? d.lda : d.K;
-  const int ldb = d.ldb ? d.ldb : d.N;
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+  int lda = d.lda ? d.lda : (ta ? d.M : d.K);
+  int ldb = d.ldb ? d.ldb : (tb ? d.K : d.N);
   const int ldc = d.ldc ? d.ldc : d.N;
-  if (lda < d.K || ldb < d.N || ldc < d.N) return fail("leading dimension smaller than shape");
+  if (lda < (ta ? d.M : d.K) || ldb < (tb ? d.K : d.N) || ldc < d.N)
+    return fail("leading dimension smaller than shape");
   hipStream_t s = pick_stream(d.stream);
+  xtc_hip_tile t = d.tile;
+  int split_k = d.split_k;
+  if (t.bm == 0) {
+    int sk = 1;
+    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
+    if (split_k <= 0) split_k = sk;
+  }
+  // B stored transposed feeds the LDS-DMA kernel directly (B^T tiles are
+  // read like A tiles); every other transposed operand gets a natural copy
+  // in a staging buffer first (one HBM-bound transpose).
+  if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true))
+    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, true);
+  const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
+  if (ta) {
+    A = transposed_copy(0, A, d.K, d.M, lda, esz, s);
+    if (!A) return 1;
+    lda = d.K;
+  }
+  if (tb) {
+    B = transposed_copy(1, B, d.N, d.K, ldb, esz, s);
+    if (!B) return 1;
+    ldb = d.N;
+  }
   const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
   const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 &&
                       aligned16(A) && aligned16(B);
@@ -730,19 +833,12 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
     HIP_TRY(hipGetLastError());
     return 0;
   }
-  xtc_hip_tile t = d.tile;
-  int split_k = d.split_k;
-  if (t.bm == 0) {
-    int sk = 1;
-    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
-    if (split_k <= 0) split_k = sk;
-  }
   const GemmEntry* e = find_entry(d.dtype, 0, t);
   if (!e)
     return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
-  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
-    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s);
+  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, false))
+    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, false);
   if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
     return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   GemmArgs a;

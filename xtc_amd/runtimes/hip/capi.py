@@ -67,6 +67,8 @@ class MatmulDesc(ctypes.Structure):
         ("relu", ctypes.c_int),
         ("relu_threshold", ctypes.c_float),
         ("stream", ctypes.c_void_p),
+        ("trans_a", ctypes.c_int),
+        ("trans_b", ctypes.c_int),
     ]
 
 

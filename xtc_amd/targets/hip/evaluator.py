@@ -60,11 +60,17 @@ class HipEvaluator(Evaluator):
     def module(self) -> Any:
         return self._module
 
-    def _host_parameters(self) -> tuple[list[np.ndarray], list[np.ndarray], list[str], list[str]]:
+    def _host_parameters(
+        self,
+    ) -> tuple[list[np.ndarray], list[np.ndarray], list[str], list[str], list[list[int] | None]]:
+        """Logical host arrays, dtypes and the inputs' layouts (a [1, 0]
+        input is stored transposed on the device, as the reference's NDArray
+        does for a layout spec, src/xtc/utils/evaluation.py:78-100)."""
         ins_spec = self._np_inputs_spec()
         outs_spec = self._np_outputs_spec()
         in_dt = [s["dtype"] for s in ins_spec]
         out_dt = [s["dtype"] for s in outs_spec]
+        layouts = [s.get("layout") for s in ins_spec]
         if self._parameters is None:
             ins = [np_init(s["shape"], s["dtype"]) for s in ins_spec]
             make = np.zeros if self._init_zero else np.empty
@@ -72,7 +78,7 @@ class HipEvaluator(Evaluator):
         else:
             ins = [np.asarray(getattr(a, "numpy", lambda a=a: a)()) for a in self._parameters[0]]
             outs = [np.asarray(getattr(a, "numpy", lambda a=a: a)()) for a in self._parameters[1]]
-        return ins, outs, in_dt, out_dt
+        return ins, outs, in_dt, out_dt, layouts
 
     def _status(self) -> tuple[int, str]:
         status = self._device.module_symbol(self._module, f"{self._module.payload_name}_status")
@@ -92,8 +98,8 @@ class HipEvaluator(Evaluator):
         dev.load_module(self._module)
         func = dev.get_module_function(self._module, self._module.payload_name)
         func.restype = None
-        ins, outs, in_dt, out_dt = self._host_parameters()
-        d_ins = [DeviceArray.from_numpy(a, dt, dev) for a, dt in zip(ins, in_dt)]
+        ins, outs, in_dt, out_dt, layouts = self._host_parameters()
+        d_ins = [DeviceArray.from_numpy(a, dt, dev, lay) for a, dt, lay in zip(ins, in_dt, layouts)]
         d_outs = [DeviceArray(a.shape, dt, dev) for a, dt in zip(outs, out_dt)]
         if self._init_zero:
             for d in d_outs:
