@@ -236,6 +236,50 @@ def test_schedule_records_primitives():
         sch.tile("q", {"q1": 2})
 
 
+def _pad_conv_mini():
+    # tests/filecheck/backends/tensor_dialect/test_pad_conv2d_mlir_tensor_fused.py
+    a = O.tensor((1, 8, 8, 3), "float32", name="I")
+    b = O.tensor((5, 5, 3, 16), "float32", name="W")
+    with O.graph(name="pad_conv2d_nhwc_mini") as gb:
+        p = O.pad2d(a, padding=2, axes=(1, 2), name="pad")
+        O.conv2d(p, b, stride=(2, 2), name="conv")
+    return gb.graph
+
+
+def test_fuse_producer_at_pad_into_conv(tmp_path):
+    backend = Backend(_pad_conv_mini())
+    sch = backend.get_scheduler()
+    sch.interchange(["b", "h", "w", "r", "s", "c", "f"])
+    sch.fuse_producer_at("w", 0)
+    sch.vectorize(["f"])
+    sched = sch.schedule()
+    assert sched.node("conv").fused == [("./w", 0)]
+    module = backend.get_compiler(dump_file=str(tmp_path / "pc")).compile(sched)
+    (ln,) = module.plan.launches
+    assert ln.kind == "conv2d" and ln.absorbed == ["pad"]
+    with pytest.raises(ScheduleError):
+        sch.fuse_producer_at("q", 0)  # not a loop of conv
+
+
+def test_fuse_producer_at_rejects_what_is_not_fused(tmp_path):
+    # input 1 (the weights) is a graph input: nothing to fuse
+    backend = Backend(_pad_conv_mini())
+    sch = backend.get_scheduler()
+    sch.fuse_producer_at("w", 1)
+    with pytest.raises(ScheduleError, match="graph input"):
+        backend.get_compiler(dump_file=str(tmp_path / "a")).compile(sch.schedule())
+    # a relu producer of a matmul is its own launch
+    x = O.tensor((64, 64), "float32", name="X")
+    w = O.tensor((64, 64), "float32", name="W")
+    with O.graph(name="relu_mm") as gb:
+        O.matmul(O.relu(x, name="act"), w, name="mm")
+    backend = Backend(gb.graph)
+    sch = backend.get_scheduler(default_node="mm")
+    sch.fuse_producer_at("i", 0)
+    with pytest.raises(ScheduleError, match="cannot fuse relu act"):
+        backend.get_compiler(dump_file=str(tmp_path / "b")).compile(sch.schedule())
+
+
 def test_meshes_are_rejected():
     sch = Backend(_matmul(64, 64, 64)).get_scheduler()
     for call in (lambda: sch.define_processor_mesh({"x": 2}), lambda: sch.define_memory_mesh({"x": 2}),

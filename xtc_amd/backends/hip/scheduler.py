@@ -232,6 +232,7 @@ class HipScheduler(Scheduler):
         self._current.pack_at[loop_name(root, axis)] = (int(input_idx), mtype, pad)
 
     def fuse_producer_at(self, axis: str, input_idx: int, root: str = DEFAULT_ROOT) -> None:
+        self._current._dim_of(axis)  # raises on an unknown loop
         self._current.fused.append((loop_name(root, axis), int(input_idx)))
 
     def _single_gpu(self, what: str) -> None:
