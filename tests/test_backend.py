@@ -401,8 +401,8 @@ def test_generated_payload_checks_status_between_launches():
 
 # ---------------------------------------------------------------- C-ABI library
 
-def _header_functions() -> set[str]:
-    text = (ROOT / "include" / "xtc_hip.h").read_text()
+def _header_functions(header: str = "xtc_hip.h") -> set[str]:
+    text = (ROOT / "include" / header).read_text()
     return set(re.findall(r"\b(xtc_hip_\w+)\s*\(", text))
 
 
@@ -413,6 +413,20 @@ def test_library_exports_every_declared_function():
     missing = [f for f in declared if not hasattr(lib, f)]
     assert not missing
     assert declared == set(capi.SIGNATURES)
+
+
+def test_pmu_library_exports_every_declared_function():
+    from xtc_amd.runtimes.hip import pmu
+
+    lib = pmu.lib()  # loads without a GPU; nothing is called
+    declared = _header_functions("xtc_hip_pmu.h")
+    assert len(declared) == 9
+    assert not [f for f in declared if not hasattr(lib, f)]
+    assert declared == set(pmu._SIGNATURES)
+    # every header under include/ is covered by one of the two libraries
+    assert {h.name for h in (ROOT / "include").glob("*.h")} == {"xtc_hip.h", "xtc_hip_pmu.h"}
+    assert pmu.is_hardware_counter("gpu.SQ_WAVES") and pmu.is_hardware_counter("gpu.cycles")
+    assert not pmu.is_hardware_counter("gpu.time") and not pmu.is_hardware_counter("cycles")
 
 
 def test_instances_and_default_tile():

@@ -1,0 +1,98 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""GPU hardware counters through the evaluator's pmu_counters, as the
+reference's tests/filecheck/evaluation/test_matmul_pmu_counters_gpu.py:34-59
+asks them of CUPTI.  rocprofiler-sdk accepts the counter tool only before
+the ROCm runtime starts, so each case runs in a fresh Python process.
+
+Pinned values: SQ_WAVES counts the waves a call launches, which the tile
+fixes (64 workgroups x 4 waves for 512^3 with 64x64 tiles and 2x2 waves);
+gpu.cycles reads GRBM_GUI_ACTIVE (the same slot, the same value); an unknown
+counter reads -1, as the reference reports an event it cannot open.
+"""
+
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+
+COUNTED = r"""
+import json, sys
+sys.path.insert(0, {root!r})
+from xtc_amd.runtimes.hip import pmu
+pmu.enable()                       # before anything touches the GPU
+import xtc_amd.graphs.xtc.op as O
+from xtc_amd.backends.hip import Backend
+
+a = O.tensor((512, 512), "float32", name="A")
+b = O.tensor((512, 512), "float32", name="B")
+with O.graph(name="matmul_pmu") as gb:
+    O.matmul(a, b, name="C")
+backend = Backend(gb.graph)
+sch = backend.get_scheduler()
+sch.tile("i", {{"i1": 64, "i2": 32}})
+sch.tile("j", {{"j1": 64, "j2": 32}})
+sch.tile("k", {{"k1": 16}})
+module = backend.get_compiler().compile(sch.schedule())
+print("[pmu] kernel", module.configs["C"].describe(), flush=True)
+counters = ["gpu.time", "gpu.cycles", "gpu.SQ_WAVES", "gpu.GRBM_GUI_ACTIVE", "gpu.NOT_A_COUNTER"]
+res, code, msg = module.get_evaluator(validate=True, pmu_counters=counters, repeat=2, number=1,
+                                      min_repeat_ms=0).evaluate()
+names = pmu.available_counters(0)
+print(json.dumps({{"code": code, "msg": msg, "res": res, "n_avail": len(names),
+                  "has": [n for n in ("SQ_WAVES", "GRBM_GUI_ACTIVE", "FETCH_SIZE") if n in names]}}), flush=True)
+"""
+
+LATE = r"""
+import json, sys
+sys.path.insert(0, {root!r})
+from xtc_amd.runtimes.hip.buffer import ensure_device
+ensure_device(0)                   # the runtime starts first
+import xtc_amd.graphs.xtc.op as O
+from xtc_amd.backends.hip import Backend
+a = O.tensor((64, 64), "float32", name="A")
+b = O.tensor((64, 64), "float32", name="B")
+with O.graph(name="matmul_late") as gb:
+    O.matmul(a, b, name="C")
+backend = Backend(gb.graph)
+module = backend.get_compiler().compile(backend.get_scheduler().schedule())
+res, code, msg = module.get_evaluator(pmu_counters=["gpu.SQ_WAVES"], repeat=1, number=1, min_repeat_ms=0).evaluate()
+res2, code2, msg2 = module.get_evaluator(pmu_counters=["gpu.time"], repeat=1, number=1, min_repeat_ms=0).evaluate()
+print(json.dumps({{"code": code, "msg": msg, "code2": code2, "res2": res2}}), flush=True)
+"""
+
+
+def _run(script: str) -> dict:
+    proc = subprocess.run([sys.executable, "-u", "-c", script.format(root=str(ROOT))], capture_output=True, text=True,
+                          timeout=240)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    line = [l for l in proc.stdout.splitlines() if l.startswith("{")][-1]
+    return json.loads(line)
+
+
+def test_gpu_counters_per_call():
+    out = _run(COUNTED)
+    assert out["code"] == 0, out["msg"]
+    assert out["n_avail"] > 50 and out["has"] == ["SQ_WAVES", "GRBM_GUI_ACTIVE", "FETCH_SIZE"]
+    res = out["res"]
+    assert len(res) == 2 * 5
+    for r in range(2):
+        t, cycles, waves, gui, unknown = res[5 * r : 5 * r + 5]
+        assert 0 < t < 1e-3
+        assert waves == 64 * 4
+        assert cycles == gui and cycles > 0
+        assert unknown == -1
+
+
+def test_gpu_counters_need_enable_before_the_runtime():
+    out = _run(LATE)
+    assert out["code"] == 2 and "before the first GPU call" in out["msg"]
+    # the event counters need no tool
+    assert out["code2"] == 0 and len(out["res2"]) == 1 and out["res2"][0] > 0

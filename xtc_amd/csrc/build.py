@@ -1,5 +1,6 @@
 # SPDX-License-Identifier: BSD-3-Clause
-"""Build of libxtc_hip.so (gfx950).
+"""Build of libxtc_hip.so (gfx950) and libxtc_hip_pmu.so (host code, GPU
+counters through rocprofiler-sdk).
 
 The GEMM/conv kernel template (gemm.hpp) is instantiated for the tile
 configurations listed by `instances()`; the instances are spread over several
@@ -7,6 +8,7 @@ generated translation units compiled in parallel, plus a registry unit that
 concatenates their entry tables.  Everything lands in-tree:
   xtc_amd/_build/   generated sources and objects
   xtc_amd/lib/libxtc_hip.so
+  xtc_amd/lib/libxtc_hip_pmu.so
 
 Usage: python -m xtc_amd.csrc.build [-j JOBS] [-v]
 """
@@ -28,6 +30,8 @@ ROOT = PKG.parent
 BUILD = PKG / "_build"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libxtc_hip.so"
+PMU_LIB = LIBDIR / "libxtc_hip_pmu.so"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 INCLUDE = ROOT / "include"
 
 ARCH = "gfx950"
@@ -262,9 +266,38 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-6000:]}")
     os.replace(tmp, LIB)
+    build_pmu(verbose)
     if verbose:
         print(f"built {LIB} ({len(instances())} kernel instances) in {time.time() - t0:.1f}s")
     return LIB
+
+
+def build_pmu(verbose: bool = False) -> Path:
+    """libxtc_hip_pmu.so: plain C++ against rocprofiler-sdk (no device code)."""
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    tmp = PMU_LIB.with_suffix(".so.tmp")
+    cmd = [
+        shutil.which("g++") or "g++",
+        "-std=c++17",
+        "-O2",
+        "-fPIC",
+        "-shared",
+        f"-I{ROCM / 'include'}",
+        f"-I{INCLUDE}",
+        str(CSRC / "pmu.cpp"),
+        f"-L{ROCM / 'lib'}",
+        "-lrocprofiler-sdk",
+        f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-o",
+        str(tmp),
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"libxtc_hip_pmu build failed:\n{res.stderr[-6000:]}")
+    os.replace(tmp, PMU_LIB)
+    return PMU_LIB
 
 
 def main(argv: list[str] | None = None) -> int:

@@ -3,6 +3,7 @@
 // HBM-bound kernels and the timing harness behind include/xtc_hip.h.
 #include <hip/hip_runtime.h>
 
+#include <dlfcn.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -999,6 +1000,33 @@ static inline void call_payload(void (*func)(void), void** args, int nargs) {
   ((fn8)func)(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Entry points of libxtc_hip_pmu.so (include/xtc_hip_pmu.h), found in the
+// process when it was loaded with global symbols and its tool initialised.
+struct PmuHooks {
+  int (*ready)(void);
+  int (*open)(int, int, const char**, int*);
+  int (*start)(void);
+  int (*stop)(double*, int);
+  void (*close)(void);
+};
+
+bool pmu_hooks(PmuHooks* h) {
+  h->ready = (int (*)(void))dlsym(RTLD_DEFAULT, "xtc_hip_pmu_ready");
+  h->open = (int (*)(int, int, const char**, int*))dlsym(RTLD_DEFAULT, "xtc_hip_pmu_open");
+  h->start = (int (*)(void))dlsym(RTLD_DEFAULT, "xtc_hip_pmu_start");
+  h->stop = (int (*)(double*, int))dlsym(RTLD_DEFAULT, "xtc_hip_pmu_stop");
+  h->close = (void (*)(void))dlsym(RTLD_DEFAULT, "xtc_hip_pmu_close");
+  return h->ready && h->open && h->start && h->stop && h->close && h->ready();
+}
+
+}  // namespace
+
+extern "C" {
+
 void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_names[],
                            int repeat, int number, int min_repeat_ms, void (*func)(void),
                            void** args, int nargs) {
@@ -1007,13 +1035,27 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
     fail("evaluate_perf: invalid arguments");
     return;
   }
-  // event kinds: 0 unknown, 1 gpu.time (s), 2 gpu.clocks (ns)
+  // event kinds: 0 unknown, 1 gpu.time (s), 2 gpu.clocks (ns), 3 hardware
+  // counter gpu.<name> (gpu.cycles = GRBM_GUI_ACTIVE, the GPU's busy cycles)
+  // read through libxtc_hip_pmu when the process loaded and enabled it
   int kinds[16] = {0};
   if (events_num > 16) events_num = 16;
+  const char* pmu_names[16];
+  int pmu_of_event[16];
+  int pmu_slot[16];
+  int npmu = 0;
   for (int e = 0; e < events_num; ++e) {
     const char* n = events_names[e];
     kinds[e] = (n && !strcmp(n, "gpu.time")) ? 1 : (n && !strcmp(n, "gpu.clocks")) ? 2 : 0;
+    if (kinds[e] == 0 && n && !strncmp(n, "gpu.", 4)) {
+      kinds[e] = 3;
+      pmu_of_event[e] = npmu;
+      pmu_names[npmu++] = !strcmp(n + 4, "cycles") ? "GRBM_GUI_ACTIVE" : n + 4;
+    }
   }
+  PmuHooks pmu;
+  const bool pmu_on = npmu > 0 && pmu_hooks(&pmu) && pmu.open(g_current, npmu, pmu_names, pmu_slot) == 0;
+  double pmu_sums[16] = {0};
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   const bool use_events = events_num > 0 && current_state();
   if (use_events) {
@@ -1029,7 +1071,9 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
     int attempts = number;
     double elapsed;
     float dev_ms = 0.f;
+    bool pmu_ok = pmu_on;
     while (1) {
+      if (pmu_on) pmu_ok = pmu.start() == 0;
       if (use_events) hipEventRecord(ev0, current_state()->stream);
       double t0 = now_s();
       for (int a = 0; a < attempts; ++a) call_payload(func, args, nargs);
@@ -1039,6 +1083,10 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
         hipEventSynchronize(ev1);
         hipEventElapsedTime(&dev_ms, ev0, ev1);
       }
+      if (pmu_on) {
+        hipDeviceSynchronize();  // every dispatch of the window has completed
+        pmu_ok = pmu.stop(pmu_sums, 16) == 0 && pmu_ok;
+      }
       if (elapsed * 1000.0 >= (double)min_repeat_ms) break;
       attempts *= 2;
     }
@@ -1047,12 +1095,15 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
         double v = -1.0;
         if (use_events && kinds[e] == 1) v = (double)dev_ms * 1e-3 / attempts;
         if (use_events && kinds[e] == 2) v = (double)dev_ms * 1e6 / attempts;
+        if (kinds[e] == 3 && pmu_ok && pmu_slot[pmu_of_event[e]] >= 0)
+          v = pmu_sums[pmu_slot[pmu_of_event[e]]] / attempts;
         results[r * events_num + e] = v;
       }
     } else {
       results[r] = elapsed / attempts;
     }
   }
+  if (pmu_on) pmu.close();
   if (use_events) {
     hipEventDestroy(ev0);
     hipEventDestroy(ev1);

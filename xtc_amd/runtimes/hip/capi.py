@@ -9,6 +9,7 @@ for any operator.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 from typing import Any
@@ -189,6 +190,10 @@ def library_available() -> bool:
 def lib() -> ctypes.CDLL:
     """The loaded libxtc_hip.so with typed entry points."""
     global _lib
+    if _lib is None and os.environ.get("XTC_HIP_PMU") == "1":
+        from . import pmu  # GPU counters: the tool must register before the runtime starts
+
+        pmu.enable()
     with _lock:
         if _lib is None:
             if not LIB_PATH.exists():

@@ -13,6 +13,11 @@ interpreter with np.allclose (src/xtc/utils/evaluation.py:129-145) ->
 timing with the evaluate_perf protocol -> unload -> copy outputs back into
 caller-provided arrays.  Returns (per-repeat seconds per call, code, msg);
 code 1 on a validation mismatch, 2 on a HIP/payload error.
+With pmu_counters the results are, per repeat, one value per counter, per
+call (src/xtc/csrcs/runtimes/host/evaluate_perf.c:63-125): "gpu.time" /
+"gpu.clocks" from HIP events, "gpu.cycles" and "gpu.<counter>" from the
+hardware counters of xtc_amd.runtimes.hip.pmu (-1 for a counter the device
+does not have, as the reference reports an event it cannot open).
 
 Differences by design: tensors live in HBM during timing (the reference maps
 host memory for device access); `rtol`/`atol` may override np.allclose's
@@ -28,7 +33,7 @@ from typing import Any
 import numpy as np
 
 from ...itf.exec import Evaluator, Executor
-from ...runtimes.hip import capi
+from ...runtimes.hip import capi, pmu
 from ...runtimes.hip.device import HipDevice
 from ...runtimes.hip.ndarray import DeviceArray
 from ...utils.bf16 import host_dtype
@@ -94,7 +99,18 @@ class HipEvaluator(Evaluator):
 
     def evaluate(self) -> tuple[list[float], int, str]:
         dev = self._device
+        hw = [c for c in self._pmu_counters if pmu.is_hardware_counter(c)]
+        if hw and not pmu.registered():
+            try:
+                pmu.enable()
+            except pmu.PmuError as err:
+                return ([], 2, f"Error in execution: GPU counters {hw} need xtc_amd.runtimes.hip.pmu.enable() "
+                               f"(or XTC_HIP_PMU=1) before the first GPU call of the process: {err}")
         dev.init_device()
+        if hw and not pmu.ready():
+            why = pmu.last_error() or "the counter tool did not initialise (the ROCm runtime of this process " \
+                "started before xtc_amd.runtimes.hip.pmu.enable())"
+            return ([], 2, f"Error in execution: GPU counters {hw} unavailable: {why}")
         dev.load_module(self._module)
         func = dev.get_module_function(self._module, self._module.payload_name)
         func.restype = None
