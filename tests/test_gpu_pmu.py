@@ -85,7 +85,9 @@ def test_gpu_counters_per_call():
     assert len(res) == 2 * 5
     for r in range(2):
         t, cycles, waves, gui, unknown = res[5 * r : 5 * r + 5]
-        assert 0 < t < 1e-3
+        # counter collection serialises and instruments every dispatch, so
+        # the device time per call is perturbed (ms, not the us of a plain run)
+        assert 0 < t < 0.1
         assert waves == 64 * 4
         assert cycles == gui and cycles > 0
         assert unknown == -1

@@ -15,7 +15,9 @@
 //     loaded once into LDS (pad_value outside the image), pixel stride 68
 //     floats so the 16 pixels read by a lane group fall on distinct banks;
 //   * the weights stream one tap (r, s) [64 c][64 f] = 16 KB at a time
-//     through 3 LDS stages by LDS DMA, two taps ahead; the 16-byte chunks of
+//     through 3 LDS stages by LDS DMA (issued from asm, lds_dma.hpp, so the
+//     compiler's waits on the LDS operand reads stay exact), two taps
+//     ahead; the 16-byte chunks of
 //     weight row c are XOR-swizzled by 4*((c>>2)&3) so the scalar B reads of
 //     the four lane groups hit disjoint banks;
 //   * 4 waves (2x2), each 32 pixels x 32 filters of v_mfma_f32_16x16x4_f32;
@@ -25,6 +27,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "lds_dma.hpp"
 
 namespace xtc_hip {
 
@@ -112,23 +116,31 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     const float* base = a.Wt + ((size_t)tap * a.C + chunk * CB) * a.F;
 #pragma unroll
     for (int i = 0; i < DMA_PER_WAVE; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(base + (size_t)w_row[i] * a.F + w_col[i]),
-                                       (lds_void*)(st + (wave * DMA_PER_WAVE + i) * 1024), 16, 0, 0);
+      lds_dma16((const void*)(base + (size_t)w_row[i] * a.F + w_col[i]), st + (wave * DMA_PER_WAVE + i) * 1024);
   };
 
+  // All of a thread's halo loads are issued before its first LDS write (at
+  // most HALO_MAX_PIX * 16 / 256 = 8 chunks), so the load latency is paid
+  // once rather than once per chunk.
   auto load_halo = [&](int chunk) {
+    constexpr int MAXQ = (HALO_MAX_PIX * (CB / 4) + 255) / 256;
     const int n16 = HH * HW * (CB / 4);  // 16-byte chunks
-    for (int q = tid; q < n16; q += 256) {
+    f32x4 v[MAXQ];
+#pragma unroll
+    for (int j = 0; j < MAXQ; ++j) {
+      const int q = tid + j * 256;
       const int pix = q >> 4;
       const int cc = (q & 15) * 4;
       const int hy = pix / HW, hx = pix - (pix / HW) * HW;
       const int ih = ih0 + hy, iw = iw0 + hx;
-      f32x4 v;
-      if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-        v = *(const f32x4*)(a.I + (((size_t)img * a.H + ih) * a.W + iw) * a.C + chunk * CB + cc);
-      else
-        v = f32x4{a.pad_value, a.pad_value, a.pad_value, a.pad_value};
-      *(f32x4*)(halo + pix * CP + cc) = v;
+      v[j] = f32x4{a.pad_value, a.pad_value, a.pad_value, a.pad_value};
+      if (q < n16 && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+        v[j] = *(const f32x4*)(a.I + (((size_t)img * a.H + ih) * a.W + iw) * a.C + chunk * CB + cc);
+    }
+#pragma unroll
+    for (int j = 0; j < MAXQ; ++j) {
+      const int q = tid + j * 256;
+      if (q < n16) *(f32x4*)(halo + (q >> 4) * CP + (q & 15) * 4) = v[j];
     }
   };
 

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lds_dma.hpp"
 #include "splitk.hpp"
 
 namespace xtc_hip {
@@ -101,7 +102,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
     const int p = (kb % A_KB_PER_ROW) * 64 + lane;
     const int src_row = r < args.M ? r : args.M - 1;
     const __bf16* src = args.A + (size_t)src_row * args.lda + k0 + (p ^ swz_a(r)) * 8;
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(sa + kb * 1024), 16, 0, 0);
+    lds_dma16((const void*)src, sa + kb * 1024);
   }
 
   // ---- B slabs: instruction i of wave w fills k-rows 4(4w+i) .. +3 of a
@@ -120,8 +121,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
     const __bf16* bb = b_base + (size_t)kt * b_step;
 #pragma unroll
     for (int i = 0; i < B_DMA_PER_WAVE; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(bb + b_off[i]),
-                                       (lds_void*)(st + (wave * B_DMA_PER_WAVE + i) * 1024), 16, 0, 0);
+      lds_dma16((const void*)(bb + b_off[i]), st + (wave * B_DMA_PER_WAVE + i) * 1024);
   };
 
   // ---- fragment coordinates
