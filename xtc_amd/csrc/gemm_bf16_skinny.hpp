@@ -7,14 +7,16 @@
 //   * a workgroup owns BN = 128 columns and a KC-deep chunk of K (split-K);
 //     the grid (N/128 x K/KC) gives each CU a few independent 256-byte-wide
 //     B row streams;
-//   * its A slice [16][KC] is copied to LDS once (LDS DMA) and stays there;
 //   * B flows through STAGES LDS stages of 64 k-rows x 256 B by LDS DMA
 //     (global_load_lds_dwordx4), STAGES-1 slabs ahead of the reads, one
 //     vmcnt wait and one barrier per slab;
-//   * 4 waves each own 32 columns; per 32-deep k-step a wave reads one A
-//     fragment (ds_read_b128) and two B fragments (ds_read_b64_tr_b16) and
-//     issues two v_mfma_f32_16x16x32_bf16 (B fragment first, so a lane holds
-//     4 consecutive columns of one row);
+//   * A (16 x 64 per slab, 2 KB, an L2 hit after the first workgroup of a
+//     split) is loaded by every wave straight into the MFMA fragment
+//     registers together with the B slab: no LDS slice, no A reads from LDS;
+//   * 4 waves each own 32 columns; per 32-deep k-step a wave reads two B
+//     fragments (ds_read_b64_tr_b16) and issues two
+//     v_mfma_f32_16x16x32_bf16 (B fragment first, so a lane holds 4
+//     consecutive columns of one row);
 //   * split-K partials go to a workspace [K/KC][16][N] (agent-scope stores);
 //     the workgroup that stores the last partial of a column block sums them
 //     in split order and applies bias / relu (splitk.hpp), so the result is
@@ -24,7 +26,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "lds_dma.hpp"
 #include "splitk.hpp"
 
 namespace xtc_hip {
@@ -51,7 +52,6 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
 constexpr int BN = 128, BK = 64, WAVES = 4;
 constexpr int B_STAGE = BK * BN * 2;  // 16 KB: 64 k-rows of 256 B
@@ -59,8 +59,6 @@ constexpr int B_STAGE = BK * BN * 2;  // 16 KB: 64 k-rows of 256 B
 // 32-byte chunk swizzle of a 256-byte B row: the rows 8g + {0..3} and
 // 8g + 8 + {0..3} read by one half-wave land on 8 distinct chunks.
 __device__ __forceinline__ int swz_b(int k) { return (k & 3) | ((k >> 1) & 4); }
-// 16-byte chunk swizzle of an A row (rows are 2*KC bytes apart).
-__device__ __forceinline__ int swz_a(int row) { return row & 7; }
 
 constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 
@@ -69,16 +67,14 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n 
 template <int KC, int STAGES>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16_skinny(SkinnyArgs args) {
   using namespace skinny;
-  constexpr int A_BYTES = 16 * KC * 2;
-  constexpr int A_KB_PER_ROW = 2 * KC / 1024;
-  constexpr int A_DMA_PER_WAVE = 16 * A_KB_PER_ROW / WAVES;
   constexpr int B_DMA_PER_WAVE = B_STAGE / 1024 / WAVES;  // 4
+  constexpr int A_LOADS = BK / 32;                        // 16-byte A loads per lane and slab
+  constexpr int PER_SLAB = A_LOADS + B_DMA_PER_WAVE;      // vector-memory ops per wave and slab
   constexpr int NK = KC / BK;
-  static_assert(KC % 512 == 0 && A_DMA_PER_WAVE * WAVES == 16 * A_KB_PER_ROW, "A split");
+  static_assert(KC % BK == 0, "split depth");
   static_assert(STAGES >= 2 && STAGES <= 4 && NK >= STAGES, "stages");
-  static_assert((STAGES - 2) * B_DMA_PER_WAVE < 64, "vmcnt range");
+  static_assert((STAGES - 2) * PER_SLAB < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) unsigned char sa[A_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char st0[B_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char st1[B_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char st2[STAGES > 2 ? B_STAGE : 16];
@@ -92,18 +88,8 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
   const int split = blockIdx.x / args.nblocks;
   const int n0 = nb * BN;
   const int k0 = split * KC;
-
-  // ---- A slice [16][KC] -> LDS, row r at r * 2KC bytes; LDS chunk p of a
-  // row holds global chunk p ^ swz_a(r).
-#pragma unroll
-  for (int i = 0; i < A_DMA_PER_WAVE; ++i) {
-    const int kb = wave * A_DMA_PER_WAVE + i;  // kilobyte of the slice
-    const int r = kb / A_KB_PER_ROW;
-    const int p = (kb % A_KB_PER_ROW) * 64 + lane;
-    const int src_row = r < args.M ? r : args.M - 1;
-    const __bf16* src = args.A + (size_t)src_row * args.lda + k0 + (p ^ swz_a(r)) * 8;
-    lds_dma16((const void*)src, sa + kb * 1024);
-  }
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
 
   // ---- B slabs: instruction i of wave w fills k-rows 4(4w+i) .. +3 of a
   // stage; lane l -> row +l/16, 16-byte slot l%16, holding global 32-byte
@@ -117,16 +103,25 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
   }
   const __bf16* b_base = args.B + (size_t)k0 * args.ldb + n0;
   const size_t b_step = (size_t)BK * args.ldb;
-  auto issue_slab = [&](int kt, unsigned char* st) {
+  // ---- A fragments straight into registers: lane (l16, g) of every wave
+  // holds A[l16][k .. k+7] for k = 32 ks + 8 g of each slab.
+  const int a_row = l16 < args.M ? l16 : args.M - 1;
+  const __bf16* a_base = args.A + (size_t)a_row * args.lda + k0 + 8 * g;
+  u32x4 ar[STAGES][A_LOADS];
+  // A loads first, then the B DMAs: the compiler counts both (the builtin
+  // DMA is a vector-memory op it knows), so its own waits for ar[] are exact.
+  auto issue_slab = [&](int kt, const int si) {
+#pragma unroll
+    for (int h = 0; h < A_LOADS; ++h) ar[si][h] = *(const u32x4*)(a_base + kt * BK + 32 * h);
     const __bf16* bb = b_base + (size_t)kt * b_step;
+    unsigned char* st = stages[si];
 #pragma unroll
     for (int i = 0; i < B_DMA_PER_WAVE; ++i)
-      lds_dma16((const void*)(bb + b_off[i]), st + (wave * B_DMA_PER_WAVE + i) * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)(bb + b_off[i]),
+                                       (lds_void*)(st + (wave * B_DMA_PER_WAVE + i) * 1024), 16, 0, 0);
   };
 
   // ---- fragment coordinates
-  const int l16 = lane & 15;
-  const int g = lane >> 4;
   const int b_krow0 = 8 * g + (l16 >> 2);
   const int b_f = swz_b(b_krow0);
   const int b_c0 = wave * 2;  // first 32-byte chunk (16 columns) of the wave
@@ -134,22 +129,22 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) gemm_bf16
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue_slab(s, stages[s]);
+  for (int s = 0; s < STAGES - 1; ++s) issue_slab(s, s);
 
   auto step = [&](int kt, const int s) {
-    // the A slice was issued first, so it has landed whenever slab 0 has
+    // this wave's ops of slab kt are done once at most those of the slabs
+    // issued after it are outstanding; the barrier then covers every wave's
+    // DMAs into stage s
     if (kt + STAGES - 2 < NK)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * B_DMA_PER_WAVE));
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * PER_SLAB));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
-    if (kt + STAGES - 1 < NK) issue_slab(kt + STAGES - 1, stages[(s + STAGES - 1) % STAGES]);
+    if (kt + STAGES - 1 < NK) issue_slab(kt + STAGES - 1, (s + STAGES - 1) % STAGES);
     const unsigned char* sb = stages[s];
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
-      const int kk = kt * (BK / 32) + ks;  // 32-deep k-step within the chunk
-      const int aoff = l16 * (2 * KC) + (((kk * 4 + g) ^ swz_a(l16)) * 16);
-      const bf16x8 af = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(sa + aoff));
+      const bf16x8 af = __builtin_bit_cast(bf16x8, ar[s][ks]);
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
         const int c32 = (b_c0 + jt) ^ b_f;

@@ -470,9 +470,9 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
   }
   dim3 grid((unsigned)(a.nblocks * splits));
   if (d.K / splits == 1024)
-    hipLaunchKernelGGL((gemm_bf16_skinny<1024, 3>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((gemm_bf16_skinny<1024, 4>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((gemm_bf16_skinny<512, 3>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((gemm_bf16_skinny<512, 4>), grid, dim3(256), 0, s, a);
   HIP_TRY(hipGetLastError());
   return 0;
 }
