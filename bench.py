@@ -84,7 +84,7 @@ def _graph(cfg: str):  # type: ignore[no-untyped-def]
 # Picked with loop-explore --strategy tile_hip on MI355X; nodes without an
 # entry keep the library's default tile.
 SCHEDULES = {
-    "C3a": {"C": {"tile": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 64}}}},
+    "C3a": {"C": {"tile": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}}},
     "C2": {"C": {"tile": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 16}}}},
     "C1": {"C": {"tile": {"i": {"i1": 32, "i2": 16}, "j": {"j1": 32, "j2": 16}, "k": {"k1": 128, "k2": 32}},
                  "parallelize": ["i", "j", "k"]}},

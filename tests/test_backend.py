@@ -348,7 +348,8 @@ def test_mapping_column_major_raster():
 def test_mapping_default_and_conv_roles():
     attrs, s = _sched(_matmul(8192, 8192, 8192, "bfloat16", out_dtype="float32"))
     cfg = map_gemm(attrs, False, s)
-    assert cfg.source == "default" and cfg.tile == (256, 256, 64, 2, 4)
+    # bf16 8192^3 defaults to the ping-pong LDS-DMA kernel's tile
+    assert cfg.source == "default" and cfg.tile == (256, 256, 32, 2, 4)
     # conv: b,h,w tile levels multiply into BM, f is N, r,s,c are K
     attrs, s = _sched(_conv_relu(), {"h": {"h1": 2}, "w": {"w1": 32}, "f": {"f1": 64}, "c": {"c1": 16}})
     cfg = map_gemm(attrs, True, s, "nearest")
@@ -435,9 +436,10 @@ def test_instances_and_default_tile():
     tiles = {(i["dtype"], bool(i["conv"]), tuple(i["tile"])) for i in inst}
     assert ("bfloat16", False, (256, 256, 64, 4, 2)) in tiles
     assert ("bfloat16", False, (256, 256, 64, 2, 4)) in tiles
+    assert ("bfloat16", False, (256, 256, 32, 2, 4)) in tiles
     assert any(d == "float32" and c for d, c, _ in tiles)
     tile, split = capi.default_tile("bfloat16", False, 8192, 8192, 8192)
-    assert tuple(tile) == (256, 256, 64, 2, 4) and split == 1
+    assert tuple(tile) == (256, 256, 32, 2, 4) and split == 1
 
 
 def test_evaluate_flops_is_half_the_flop_rate():

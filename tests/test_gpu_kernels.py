@@ -443,6 +443,59 @@ def test_lds_dma_bf16_swizzle_covers_every_position():
         np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
 
 
+# ------------------------------- ping-pong LDS-DMA bf16 kernel (256x256x32, 2x4)
+
+PINGPONG = (256, 256, 32, 2, 4)
+
+
+@pytest.mark.parametrize("K", [32, 64, 96, 128, 160, 1024, 1056])
+def test_pingpong_bf16_integer_exact_every_pipeline_depth(K):
+    # K / 32 slabs below, at and above the DMA lead (3) and the stage count
+    # (4), and not a multiple of it; 2x3 tiles give six different K-stagger
+    # offsets, which wrap when there are fewer slabs than the offset
+    M, N = 512, 768
+    a, b = _int_operands(M, N, K, 5)
+    out = run_matmul(a, b, "bfloat16", tile=PINGPONG)
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32), err_msg=f"K={K}")
+
+
+def test_pingpong_bf16_swizzle_covers_every_position():
+    # distinct small integers at every (row, k) / (k, col) of one slab
+    M, N, K = 256, 256, 32
+    a = ((np.arange(M)[:, None] * 3 + np.arange(K)[None, :] * 5) % 7 - 3).astype(np.float32)
+    b = ((np.arange(K)[:, None] * 11 + np.arange(N)[None, :] * 2) % 9 - 4).astype(np.float32)
+    out = run_matmul(a, b, "bfloat16", tile=PINGPONG)
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32))
+    out_t = run_matmul_layout(a, b, "bfloat16", False, True, tile=PINGPONG)
+    np.testing.assert_array_equal(out_t, ref.matmul(a, b).astype(np.float32))
+
+
+def test_pingpong_bf16_seeded_bias_relu_strided():
+    rng = np.random.default_rng(23)
+    M, N, K = 512, 512, 544
+    a = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    out = _run_strided(a, b, PINGPONG, lda=K + 64, ldb=N + 256, ldc=N + 4, relu=True, bias=bias)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_BF16
+
+
+def test_pingpong_bf16_transposed_b_matches_row_major_and_bk64():
+    # B^T read natively: same fragments in the same order as row-major B, so
+    # bit-identical; and the same K walk as the 256x256x64 kernel
+    rng = np.random.default_rng(43)
+    M, N, K = 512, 768, 1024
+    a = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    b = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    out = run_matmul_layout(a, b, "bfloat16", False, True, tile=PINGPONG, pad_a=8, pad_b=64, relu=True, bias=bias)
+    expect = ref.relu(ref.matmul(a, b) + bias)
+    assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_BF16
+    same = run_matmul_layout(a, b, "bfloat16", False, False, tile=PINGPONG, pad_a=8, pad_b=64, relu=True, bias=bias)
+    np.testing.assert_array_equal(out, same)
+
+
 # ------------------------------------------------- skinny bf16 (B-streaming kernel)
 
 SKINNY = (16, 128, 64, 1, 4)

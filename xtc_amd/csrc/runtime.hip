@@ -15,6 +15,7 @@
 
 #include "gemm_bf16_lds.hpp"
 #include "gemm_bf16_skinny.hpp"
+#include "gemm_bf16_pingpong.hpp"
 #include "conv_direct.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
@@ -346,8 +347,8 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
     }
   }
   if (!f32 && M >= 4096 && N >= 4096) {
-    // aligned shapes take the LDS-DMA kernel behind this tile
-    if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && pick(256, 256, 64, 2, 4)) return;
+    // aligned shapes take the ping-pong LDS-DMA kernel behind this tile
+    if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && pick(256, 256, 32, 2, 4)) return;
     if (pick(256, 256, 64, 2, 2)) return;
   }
   if (M >= 2048 && N >= 2048) {
@@ -395,8 +396,9 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// The LDS-DMA bf16 kernel (gemm_bf16_lds.hpp) implements the 256x256x64
-// tiles with 2x4 and 4x2 waves when the shape needs no bounds checks, for B
+// The LDS-DMA bf16 kernels implement the 256x256x64 tiles with 2x4 and 4x2
+// waves (gemm_bf16_lds.hpp) and the 256x256x32 tile with 2x4 waves
+// (gemm_bf16_pingpong.hpp) when the shape needs no bounds checks, for B
 // row-major (bt = false, ldb >= N) or stored transposed (bt = true, ldb >= K).
 // XTC_HIP_GENERIC_GEMM=1 forces the generic template (for A/B comparisons).
 bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
@@ -407,9 +409,14 @@ bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
     return v && v[0] == '1';
   }();
   if (disabled || d.dtype != XTC_HIP_BF16 || split_k > 1) return false;
-  if (t.bm != 256 || t.bn != 256 || t.bk != 64) return false;
-  if (!((t.wgm == 2 && t.wgn == 4) || (t.wgm == 4 && t.wgn == 2))) return false;
-  if (d.M % 256 || d.N % 256 || d.K % 64) return false;
+  if (t.bm != 256 || t.bn != 256) return false;
+  // bk 64: gemm_bf16_lds.hpp with 2x4 or 4x2 waves; bk 32: gemm_bf16_pingpong.hpp, 2x4
+  if (t.bk == 64) {
+    if (!((t.wgm == 2 && t.wgn == 4) || (t.wgm == 4 && t.wgn == 2))) return false;
+  } else if (t.bk != 32 || t.wgm != 2 || t.wgn != 4) {
+    return false;
+  }
+  if (d.M % 256 || d.N % 256 || d.K % t.bk) return false;
   if (lda % 8 || ldb % 8 || ldc % 4) return false;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
   // element offsets of one tile row/column range must fit in 32 bits
@@ -549,7 +556,12 @@ int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int
   a.group_m = d.group_m > 0 ? d.group_m : 8;  // 8 <= 16 at 8192^3, zero and random data
   a.xcd_remap = d.xcd_remap;
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (t.wgm == 2) {
+  if (t.bk == 32) {  // 2x4 waves: the ping-pong schedule
+    if (bt)
+      hipLaunchKernelGGL((gemm_bf16_pingpong<true, 4>), grid, dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_bf16_pingpong<false, 4>), grid, dim3(512), 0, s, a);
+  } else if (t.wgm == 2) {
     if (bt)
       hipLaunchKernelGGL((gemm_bf16_256x256<2, 4, 64, 2, true>), grid, dim3(512), 0, s, a);
     else
