@@ -16,6 +16,7 @@
 #include "gemm_bf16_lds.hpp"
 #include "gemm_bf16_skinny.hpp"
 #include "gemm_bf16_pingpong.hpp"
+#include "gemm_f32_splitwave.hpp"
 #include "conv_direct.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
@@ -446,6 +447,64 @@ bool skinny_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, in
   return true;
 }
 
+// The split-wave fp32 kernel (gemm_f32_splitwave.hpp) implements the
+// one-wave 32x32x16 tile with split-K 2..8 when the shape is aligned: the
+// splits of a tile are the waves of one workgroup instead of workgroups of
+// the grid (same partial sums, same summation order).
+bool splitwave_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
+                            const void* A) {
+  static const bool disabled = [] {
+    const char* v = getenv("XTC_HIP_GENERIC_GEMM");
+    return v && v[0] == '1';
+  }();
+  if (disabled || d.dtype != XTC_HIP_F32) return false;
+  if (t.bm != 32 || t.bn != 32 || t.bk != 16 || t.wgm != 1 || t.wgn != 1) return false;
+  if (split_k < 2 || split_k > 8) return false;
+  if (d.M % 32 || d.N % 32 || d.K % (16 * split_k)) return false;
+  if (lda % 4 || !aligned16(A)) return false;
+  return true;
+}
+
+int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
+                          const void* A, const void* B, float* C, const float* bias, hipStream_t s) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.bias = bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  a.tiles_m = d.M / 32;
+  a.tiles_n = d.N / 32;
+  a.group_m = d.group_m > 0 ? d.group_m : 8;
+  a.xcd_remap = d.xcd_remap;
+  a.k_per_split = d.K / split_k;
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  if (split_k == 2)
+    hipLaunchKernelGGL((gemm_f32_splitwave<2>), grid, dim3(128), 0, s, a);
+  else if (split_k == 3)
+    hipLaunchKernelGGL((gemm_f32_splitwave<3>), grid, dim3(192), 0, s, a);
+  else if (split_k == 4)
+    hipLaunchKernelGGL((gemm_f32_splitwave<4>), grid, dim3(256), 0, s, a);
+  else if (split_k == 5)
+    hipLaunchKernelGGL((gemm_f32_splitwave<5>), grid, dim3(320), 0, s, a);
+  else if (split_k == 6)
+    hipLaunchKernelGGL((gemm_f32_splitwave<6>), grid, dim3(384), 0, s, a);
+  else if (split_k == 7)
+    hipLaunchKernelGGL((gemm_f32_splitwave<7>), grid, dim3(448), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_f32_splitwave<8>), grid, dim3(512), 0, s, a);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
 int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
                        const void* A, const void* B, float* C, const float* bias, hipStream_t s) {
   const int splits = split_k < 1 ? 1 : split_k;
@@ -854,6 +913,8 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
     return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, false);
   if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
     return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
+  if (splitwave_gemm_applies(d, t, split_k, lda, A))
+    return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = A;
