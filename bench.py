@@ -251,8 +251,9 @@ def main(argv: list[str] | None = None) -> int:
         return _calibrate_copy(args.steps)
     if args.gpus != 1:
         print(
-            f"bench.py: --gpus {args.gpus} is not supported: every box of this pool has one GPU; "
-            "the kernel is measured on one GPU's share (see DESIGN.md for how it would shard).",
+            f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU; a GEMM "
+            "shards over GPUs by rows of A and C with B replicated, so one GPU's share is the "
+            "same kernel at M / N_gpus rows.",
             file=sys.stderr,
         )
         return 2
