@@ -126,3 +126,36 @@ def test_tile_hip_conv_points_map_exactly():
         assert (cfg.bm, cfg.bm // cfg.wgm, cfg.bn, cfg.bn // cfg.wgn, cfg.bk) == tuple(x[:5])
     # the default point is the library's own choice
     assert st.default_schedule(2)[5] >= 1
+
+
+def test_pmu_counters_are_split_from_the_times(tmp_path, monkeypatch):
+    # with counters the evaluator returns repeat x counters values, repeat by
+    # repeat in counter order; the CSV time is the min of the gpu.time ones
+    # (added first when not requested) and the DB record keeps every counter
+    seen = []
+
+    def evaluate_one(self, module):
+        seen.append(self.counters())
+        #        repeat 0           repeat 1
+        return [3e-3, 256.0, 9.0, 2e-3, 256.0, 7.0], 0, ""
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    g = build_graph("matmul", [256, 256, 256], "float32")
+    cfg = ExplorationConfig(trials=2, seed=1, output=str(tmp_path / "p.csv"), db_file=str(tmp_path / "p.jsonl"),
+                            peak_flops=1e12, pmu_counters=["gpu.SQ_WAVES", "gpu.cycles"], jobs=1)
+    res = Exploration(g, cfg).run()
+    assert seen == [["gpu.time", "gpu.SQ_WAVES", "gpu.cycles"]] * 2
+    assert [t for _, t, _, _ in res] == [[3e-3, 2e-3]] * 2
+    rows = list(csv.DictReader(open(tmp_path / "p.csv")))
+    assert [float(r["time"]) for r in rows] == [2e-3, 2e-3]
+    recs = [json.loads(l) for l in open(tmp_path / "p.jsonl")]
+    assert recs[0]["results"] == [0, [2e-3]]
+    assert recs[0]["counters"] == {"gpu.time": [3e-3, 2e-3], "gpu.SQ_WAVES": [256.0, 256.0], "gpu.cycles": [9.0, 7.0]}
+    # no counters requested: plain timing, values untouched
+    cfg.pmu_counters = []
+    ex = Exploration(g, cfg)
+    assert ex.counters() == [] and ex.split_counters([1.0, 2.0]) == ([1.0, 2.0], {})
+    # gpu.time requested explicitly keeps its place
+    cfg.pmu_counters = ["gpu.cycles", "gpu.time"]
+    assert Exploration(g, cfg).split_counters([5.0, 1e-3, 6.0, 2e-3]) == (
+        [1e-3, 2e-3], {"gpu.cycles": [5.0, 6.0], "gpu.time": [1e-3, 2e-3]})

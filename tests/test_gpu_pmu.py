@@ -98,3 +98,32 @@ def test_gpu_counters_need_enable_before_the_runtime():
     assert out["code"] == 2 and "before the first GPU call" in out["msg"]
     # the event counters need no tool
     assert out["code2"] == 0 and len(out["res2"]) == 1 and out["res2"][0] > 0
+
+
+def test_explore_records_counters_per_sample(tmp_path):
+    # loop-explore with --pmu-counters in a fresh process (XTC_HIP_PMU=1
+    # registers the counter tool when the library loads, before any GPU
+    # call): the CSV time is the min of the gpu.time values, and the DB
+    # record of every sample carries each counter's per-repeat values
+    import csv
+    import os
+
+    out, db = tmp_path / "e.csv", tmp_path / "e.jsonl"
+    env = {**os.environ, "XTC_HIP_PMU": "1"}
+    cmd = [sys.executable, "-u", "-m", "xtc_amd.cli.explore", "--operator", "matmul", "--dims", "256", "256", "256",
+           "--dtype", "float32", "--strategy", "tile_hip", "--search", "random", "--trials", "3", "--seed", "0",
+           "--repeat", "2", "--min-repeat-ms", "0", "--jobs", "2", "--output", str(out), "--db-file", str(db),
+           "--pmu-counters", "gpu.SQ_WAVES"]
+    print("[explore pmu]", " ".join(cmd[3:]), flush=True)
+    proc = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    rows = list(csv.DictReader(open(out)))
+    recs = [json.loads(l) for l in open(db)]
+    assert len(rows) == 3 and len(recs) == 3, proc.stderr[-3000:]
+    for r, rec in zip(rows, recs):
+        c = rec["counters"]
+        assert set(c) == {"gpu.time", "gpu.SQ_WAVES"} and len(c["gpu.time"]) == 2
+        assert float(r["time"]) == min(c["gpu.time"]) and 0 < float(r["time"]) < 0.1
+        # every launch has at least one workgroup of waves, and each repeat
+        # runs the same launches
+        assert c["gpu.SQ_WAVES"][0] > 0 and c["gpu.SQ_WAVES"][0] == c["gpu.SQ_WAVES"][1]

@@ -84,7 +84,10 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("--number", type=int, default=1)
     p.add_argument("--min-repeat-ms", type=int, default=100)
     p.add_argument("--validate", action="store_true")
-    p.add_argument("--pmu-counters", nargs="*", default=[])
+    p.add_argument("--pmu-counters", nargs="*", default=[],
+                   help="counters per sample (gpu.time, gpu.cycles, gpu.<rocprofiler counter>); gpu.time is "
+                        "added when missing and gives the CSV time, every counter's values go to the --db-file "
+                        "record; hardware counters need XTC_HIP_PMU=1 or a fresh process")
     p.add_argument("--jobs", type=int, default=max(1, min(16, (os.cpu_count() or 2) // 2)))
     p.add_argument("--output", default="results.csv")
     p.add_argument("--db-file")

@@ -233,12 +233,31 @@ class Exploration:
             kwargs.setdefault("schedule_policy", "strict")
         return backend.get_compiler(**kwargs).compile(sch.schedule())
 
+    def counters(self) -> list[str]:
+        """The pmu_counters each sample is evaluated with: the requested ones,
+        with "gpu.time" added first when missing so that the time column
+        stays a time.  Empty when none were requested (plain timing)."""
+        req = list(self.config.pmu_counters)
+        if req and "gpu.time" not in req:
+            req = ["gpu.time", *req]
+        return req
+
     def evaluate_one(self, module: Any) -> tuple[list[float], int, str]:
         c = self.config
         return module.get_evaluator(
             repeat=c.repeat, number=c.number, min_repeat_ms=c.min_repeat_ms, validate=c.validate,
-            pmu_counters=c.pmu_counters,
+            pmu_counters=self.counters(),
         ).evaluate()
+
+    def split_counters(self, values: list[float]) -> tuple[list[float], dict[str, list[float]]]:
+        """Evaluator values -> (times, {counter: per-repeat values}).  With
+        counters the evaluator returns them repeat by repeat, in counter order
+        (evaluate_perf's layout); the times are the "gpu.time" entries."""
+        names = self.counters()
+        if not names:
+            return values, {}
+        per = {name: values[i :: len(names)] for i, name in enumerate(names)}
+        return per["gpu.time"], per
 
     def peak_time(self) -> float:
         peak = self.config.peak_flops
@@ -282,7 +301,10 @@ class Exploration:
                     module = fut.result()
                     extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()},
                              "error": ""}
-                    times, code, msg = self.evaluate_one(module)
+                    values, code, msg = self.evaluate_one(module)
+                    times, per_counter = self.split_counters(values) if code == 0 else ([], {})
+                    if per_counter:
+                        extra["counters"] = per_counter
                 except Exception as err:  # a failed sample is recorded, not fatal
                     times, code, msg = [], 2, f"{type(err).__name__}: {err}"
                 if code:
