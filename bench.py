@@ -26,6 +26,7 @@ import argparse
 import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -308,6 +309,7 @@ def main(argv: list[str] | None = None) -> int:
         if not spot_err <= tol:
             raise SystemExit(f"parity spot check failed: scaled error {spot_err} > {tol}")
 
+    print(f"[bench] {cfg}: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step()
     capi.check(L.xtc_hip_synchronize(), "synchronize")
@@ -360,9 +362,33 @@ def main(argv: list[str] | None = None) -> int:
         },
         "roofline": roof,
     }
+    # the same schedule under XTC's own timing protocol (evaluate_perf.c:92-120):
+    # per repeat, synchronous payload calls doubled until min_repeat_ms, time
+    # per call, min and median over repeats; device time from HIP events and
+    # host wall clock.  The protocol needs the synchronising payload (the
+    # default compile): its loop measures host time.
+    print(f"[bench] {cfg}: evaluate_perf protocol", file=sys.stderr, flush=True)
+    sync_module = backend.get_compiler(schedule_policy="strict").compile(sch.schedule())
+    dev.load_module(sync_module)
+    sync_fn = dev.get_module_function(sync_module, sync_module.payload_name)
+    sync_fn.restype = None
+    sync_status = dev.module_symbol(sync_module, f"{sync_module.payload_name}_status")
+    sync_status.restype = ctypes.c_int
+    proto: dict = {"repeat": 5, "number": 1, "min_repeat_ms": 100}
+    for label, events in (("device", ["gpu.time"]), ("wall", [])):
+        vals = dev.evaluate_perf(events, 5, 1, 100, sync_fn, cargs, len(cargs))
+        proto[f"{label}_min_ms"] = round(min(vals) * 1e3, 4)
+        proto[f"{label}_median_ms"] = round(statistics.median(vals) * 1e3, 4)
+    if sync_status():
+        raise SystemExit("payload reported an error under the evaluate_perf protocol")
+    proto["device_min_pct_of_peak"] = round(100 * (
+        _alg_bytes(cfg) / (proto["device_min_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS if cfg == "C3b"
+        else flops / (proto["device_min_ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[dtype]), 2)
+    line["config"]["xtc_protocol"] = proto
     if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
         line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup)
     if not args.no_cpu:
+        print(f"[bench] {cfg}: cpu baseline", file=sys.stderr, flush=True)
         try:
             line["cpu_baseline"] = _cpu_baseline(cfg)
         except Exception as err:  # the GPU figure stands without it
