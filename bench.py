@@ -86,7 +86,7 @@ def _graph(cfg: str):  # type: ignore[no-untyped-def]
 # entry keep the library's default tile.
 SCHEDULES = {
     "C3a": {"C": {"tile": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}}},
-    "C2": {"C": {"tile": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 16}}}},
+    "C2": {"C": {"tile": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 32}}}},
     "C1": {"C": {"tile": {"i": {"i1": 32, "i2": 32}, "j": {"j1": 32, "j2": 32}, "k": {"k1": 128, "k2": 16}},
                  "parallelize": ["i", "j", "k"]}},
     "C5": {

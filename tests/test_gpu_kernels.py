@@ -496,6 +496,61 @@ def test_pingpong_bf16_transposed_b_matches_row_major_and_bk64():
     np.testing.assert_array_equal(out, same)
 
 
+# ------------------------------ LDS-DMA fp32 kernel (128x256x32 2x4, 256x128x32 4x2)
+
+F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2)]
+
+
+@pytest.mark.parametrize("tile", F32_LDS)
+@pytest.mark.parametrize("K,split", [(32, 1), (64, 1), (96, 1), (1024, 1), (1056, 1), (512, 2), (1024, 4), (2048, 8)])
+def test_f32_lds_integer_exact_every_pipeline_depth(tile, K, split):
+    # K / 32 / split slabs below, at and above the DMA lead (2); 2x2 or 2x4
+    # tiles; split-K finished in the kernel
+    M, N = 512, 512
+    a, b = _int_operands(M, N, K, 7)
+    out = run_matmul(a, b, "float32", tile=tile, split_k=split)
+    np.testing.assert_array_equal(out, ref.matmul(a, b).astype(np.float32), err_msg=f"{tile} K={K} split={split}")
+
+
+@pytest.mark.parametrize("tile", F32_LDS)
+def test_f32_lds_seeded_bias_relu_strided(tile):
+    rng = np.random.default_rng(37)
+    M, N, K = 512, 512, 640
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = rng.uniform(-1, 1, (N,)).astype(np.float32)
+    for split in (1, 2):
+        out = _run_strided_f32(a, b, tile, lda=K + 12, ldb=N + 8, ldc=N + 4, relu=True, bias=bias, split_k=split)
+        expect = ref.relu(ref.matmul(a, b) + bias)
+        assert ref.scaled_error(out, expect, K, 1.0, 1.0) <= TOL_F32, f"split {split}"
+
+
+def _run_strided_f32(a, b, tile, lda, ldb, ldc, relu=False, bias=None, split_k=1):
+    """fp32 matmul with padded leading dimensions (elements)."""
+    M, K = a.shape
+    N = b.shape[1]
+    ap = np.zeros((M, lda), np.float32)
+    ap[:, :K] = a
+    bp = np.zeros((K, ldb), np.float32)
+    bp[:, :N] = b
+    A, B = _dev(ap, "float32"), _dev(bp, "float32")
+    C = DeviceBuffer(M * ldc * 4)
+    C.zero()
+    bias_buf = DeviceBuffer.from_numpy(bias.astype(np.float32)) if bias is not None else None
+    d = capi.MatmulDesc()
+    d.dtype = capi.XTC_HIP_F32
+    d.M, d.N, d.K = M, N, K
+    d.lda, d.ldb, d.ldc = lda, ldb, ldc
+    d.tile = capi.Tile(*tile)
+    d.split_k = split_k
+    d.xcd_remap = 1
+    d.relu = int(relu)
+    L = capi.lib()
+    capi.check(L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, bias_buf.c_ptr if bias_buf else None))
+    capi.check(L.xtc_hip_synchronize())
+    return C.to_numpy((M, ldc), np.float32)[:, :N]
+
+
 # ------------------------------ split-wave fp32 kernel (32x32x16, 1x1, split-K in a workgroup)
 
 SPLITWAVE = (32, 32, 16, 1, 1)

@@ -17,6 +17,7 @@
 #include "gemm_bf16_skinny.hpp"
 #include "gemm_bf16_pingpong.hpp"
 #include "gemm_f32_splitwave.hpp"
+#include "gemm_f32_lds.hpp"
 #include "conv_direct.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
@@ -445,6 +446,34 @@ bool skinny_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, in
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
   if ((int64_t)64 * ldb > INT32_MAX) return false;
   return true;
+}
+
+// The LDS-DMA fp32 kernel (gemm_f32_lds.hpp) implements the 128x256x32 (2x4
+// waves) and 256x128x32 (4x2 waves) fp32 tiles, split-K included, when the
+// shape needs no bounds checks: one workgroup of 8 waves per CU.
+bool f32_lds_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
+                          int ldb, int ldc, const void* A, const void* B, const void* C,
+                          const void* bias) {
+  static const bool disabled = [] {
+    const char* v = getenv("XTC_HIP_GENERIC_GEMM");
+    return v && v[0] == '1';
+  }();
+  if (disabled || d.dtype != XTC_HIP_F32) return false;
+  const bool t1 = t.bm == 128 && t.bn == 256 && t.wgm == 2 && t.wgn == 4;
+  const bool t2 = t.bm == 256 && t.bn == 128 && t.wgm == 4 && t.wgn == 2;
+  if (!(t1 || t2) || t.bk != 32) return false;
+  const int splits = split_k < 1 ? 1 : split_k;
+  if (d.M % t.bm || d.N % t.bn || d.K % (32 * splits)) return false;
+  if (lda % 4 || ldb % 4 || ldc % 4) return false;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
+  // element offsets of one tile's rows must fit in 32 bits
+  if ((int64_t)t.bm * lda > INT32_MAX || (int64_t)32 * ldb > INT32_MAX) return false;
+  return true;
+}
+
+template <int BM, int BN, int WGM, int WGN>
+void launch_f32_lds(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_f32_lds<BM, BN, 32, WGM, WGN, 3>), grid, dim3(512), 0, s, a);
 }
 
 // The split-wave fp32 kernel (gemm_f32_splitwave.hpp) implements the
@@ -915,6 +944,14 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
     return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   if (splitwave_gemm_applies(d, t, split_k, lda, A))
     return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
+  GemmEntry lds_entry;
+  if (f32_lds_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias)) {
+    // same tiles, split-K set-up and grid as the generic instance; only the
+    // kernel differs
+    lds_entry = *e;
+    lds_entry.launch = t.wgm == 2 ? &launch_f32_lds<128, 256, 2, 4> : &launch_f32_lds<256, 128, 4, 2>;
+    e = &lds_entry;
+  }
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = A;
