@@ -438,6 +438,9 @@ def test_instances_and_default_tile():
     assert ("bfloat16", False, (256, 256, 64, 2, 4)) in tiles
     assert ("bfloat16", False, (256, 256, 32, 2, 4)) in tiles
     assert any(d == "float32" and c for d, c, _ in tiles)
+    # large aligned fp32: the LDS-DMA fp32 kernel's tile when it fills the chip
+    assert tuple(capi.default_tile("float32", False, 4096, 4096, 4096)[0]) == (256, 128, 32, 4, 2)
+    assert tuple(capi.default_tile("float32", False, 2048, 2048, 2048)[0]) == (128, 128, 32, 2, 2)
     tile, split = capi.default_tile("bfloat16", False, 8192, 8192, 8192)
     assert tuple(tile) == (256, 256, 32, 2, 4) and split == 1
 

@@ -353,6 +353,11 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
     if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && pick(256, 256, 32, 2, 4)) return;
     if (pick(256, 256, 64, 2, 2)) return;
   }
+  // large aligned fp32 shapes with at least one 256x128 tile per CU: the
+  // LDS-DMA fp32 kernel behind this tile
+  if (f32 && !conv && M % 256 == 0 && N % 128 == 0 && K % 32 == 0 && (int64_t)(M / 256) * (N / 128) >= 256 &&
+      pick(256, 128, 32, 4, 2))
+    return;
   if (M >= 2048 && N >= 2048) {
     if (pick(128, 128, bk, 2, 2)) return;
   }
