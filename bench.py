@@ -206,6 +206,31 @@ def _cpu_baseline(cfg: str) -> dict:
     }
 
 
+def _xtc_protocol(cfg: str, backend, sch, dev, cargs, flops: int, dtype: str) -> dict:  # type: ignore[no-untyped-def]
+    """The bench's schedule under XTC's own timing protocol
+    (evaluate_perf.c:92-120): per repeat, synchronous payload calls doubled
+    until min_repeat_ms, time per call, min and median over repeats; device
+    time from HIP events and host wall clock.  The protocol measures host
+    time, so it takes the synchronising payload (the default compile)."""
+    module = backend.get_compiler(schedule_policy="strict").compile(sch.schedule())
+    dev.load_module(module)
+    fn = dev.get_module_function(module, module.payload_name)
+    fn.restype = None
+    status = dev.module_symbol(module, f"{module.payload_name}_status")
+    status.restype = ctypes.c_int
+    proto: dict = {"repeat": 5, "number": 1, "min_repeat_ms": 100}
+    for label, events in (("device", ["gpu.time"]), ("wall", [])):
+        vals = dev.evaluate_perf(events, 5, 1, 100, fn, cargs, len(cargs))
+        proto[f"{label}_min_ms"] = round(min(vals) * 1e3, 4)
+        proto[f"{label}_median_ms"] = round(statistics.median(vals) * 1e3, 4)
+    if status():
+        raise SystemExit("payload reported an error under the evaluate_perf protocol")
+    rate = (_alg_bytes(cfg) / (proto["device_min_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS if cfg == "C3b"
+            else flops / (proto["device_min_ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[dtype])
+    proto["device_min_pct_of_peak"] = round(100 * rate, 2)
+    return proto
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -242,6 +267,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C3a", choices=["C1", "C2", "C3a", "C3b", "C4", "C5"])
+    ap.add_argument("--no-protocol", action="store_true",
+                    help="skip the evaluate_perf protocol pass (kernel traces then hold only the timed steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--vs-hipblaslt", action="store_true",
                     help="also time torch.matmul on the same inputs (matmul configs) and report it in config")
@@ -367,24 +394,9 @@ def main(argv: list[str] | None = None) -> int:
     # per call, min and median over repeats; device time from HIP events and
     # host wall clock.  The protocol needs the synchronising payload (the
     # default compile): its loop measures host time.
-    print(f"[bench] {cfg}: evaluate_perf protocol", file=sys.stderr, flush=True)
-    sync_module = backend.get_compiler(schedule_policy="strict").compile(sch.schedule())
-    dev.load_module(sync_module)
-    sync_fn = dev.get_module_function(sync_module, sync_module.payload_name)
-    sync_fn.restype = None
-    sync_status = dev.module_symbol(sync_module, f"{sync_module.payload_name}_status")
-    sync_status.restype = ctypes.c_int
-    proto: dict = {"repeat": 5, "number": 1, "min_repeat_ms": 100}
-    for label, events in (("device", ["gpu.time"]), ("wall", [])):
-        vals = dev.evaluate_perf(events, 5, 1, 100, sync_fn, cargs, len(cargs))
-        proto[f"{label}_min_ms"] = round(min(vals) * 1e3, 4)
-        proto[f"{label}_median_ms"] = round(statistics.median(vals) * 1e3, 4)
-    if sync_status():
-        raise SystemExit("payload reported an error under the evaluate_perf protocol")
-    proto["device_min_pct_of_peak"] = round(100 * (
-        _alg_bytes(cfg) / (proto["device_min_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS if cfg == "C3b"
-        else flops / (proto["device_min_ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[dtype]), 2)
-    line["config"]["xtc_protocol"] = proto
+    if not args.no_protocol:
+        print(f"[bench] {cfg}: evaluate_perf protocol", file=sys.stderr, flush=True)
+        line["config"]["xtc_protocol"] = _xtc_protocol(cfg, backend, sch, dev, cargs, flops, dtype)
     if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
         line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup)
     if not args.no_cpu:
