@@ -91,7 +91,7 @@ SCHEDULES = {
                  "parallelize": ["i", "j", "k"]}},
     "C5": {
         "fc1": {"tile": {"i": {"i1": 128, "i2": 64}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}},
-        "fc2": {"tile": {"i": {"i1": 128, "i2": 32}, "j": {"j1": 64, "j2": 64}, "k": {"k1": 1024, "k2": 16}},
+        "fc2": {"tile": {"i": {"i1": 128, "i2": 64}, "j": {"j1": 128, "j2": 32}, "k": {"k1": 2048, "k2": 32}},
                 "parallelize": ["i", "j", "k"]},
     },
 }

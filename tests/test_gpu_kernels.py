@@ -498,7 +498,7 @@ def test_pingpong_bf16_transposed_b_matches_row_major_and_bk64():
 
 # ------------------------------ LDS-DMA fp32 kernel (128x256x32 2x4, 256x128x32 4x2)
 
-F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2)]
+F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2), (128, 128, 32, 2, 4)]
 
 
 @pytest.mark.parametrize("tile", F32_LDS)

@@ -115,6 +115,10 @@ def instances() -> list[tuple[int, int, int, int, int, int, int]]:
                             continue
                         if tile_legal(dtype, 0, bm, bn, bk, wgm, wgn):
                             out.append((dtype, 0, bm, bn, bk, wgm, wgn))
+    # fp32 128x128x32 with 8 waves (2x4 of 64x32): the LDS-DMA fp32 kernel's
+    # tile for N-narrow GEMMs (runtime.hip routes aligned shapes to it)
+    if tile_legal(F32, 0, 128, 128, 32, 2, 4) and (F32, 0, 128, 128, 32, 2, 4) not in out:
+        out.append((F32, 0, 128, 128, 32, 2, 4))
     # implicit-GEMM conv loaders: the conv shapes have small N (= F channels)
     for dtype in (F32, BF16):
         bk = 32 if dtype == F32 else 64

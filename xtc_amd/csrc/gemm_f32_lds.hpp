@@ -10,8 +10,8 @@
 // with register-only loops).  The register-staged generic kernel (gemm.hpp)
 // needs two workgroups per CU to hide its global-load latency.  This kernel
 // hides it in one workgroup instead:
-//   * 8 waves (WGM x WGN) of 64x64, one workgroup per CU (the stages fill
-//     the LDS): two waves per SIMD;
+//   * 8 waves (WGM x WGN), one workgroup per CU (the stages fill the LDS):
+//     two waves per SIMD;
 //   * global -> LDS by LDS DMA (global_load_lds_dwordx4, issued from asm),
 //     STAGES stages of one BK-deep slab, D = STAGES - 1 slabs ahead of the
 //     MFMAs;
@@ -90,7 +90,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
   constexpr int B_ROWS_PER_KB = 1024 / (BN * 4);
   constexpr int B_CHUNKS = BN / 4;
   constexpr int D = STAGES - 1;
-  static_assert(WGM * WGN == 8 && TM == 4 && TN == 4, "8 waves of 64x64");
+  static_assert(WGM * WGN == 8 && TM >= 1 && TN >= 1 && TM * 16 * WGM == BM && TN * 16 * WGN == BN, "8 waves");
   static_assert(BK == 16 || BK == 32, "BK");
   static_assert(BN * 4 <= 1024 && 1024 % (BN * 4) == 0, "a DMA kilobyte holds whole B rows");
   static_assert(A_KB * 8 * 1024 == A_STAGE && B_KB * 8 * 1024 == B_STAGE, "stage must split over 8 waves");
@@ -148,9 +148,9 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
   // ---- fragment coordinates
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int a_row0 = wm * 64 + l16;    // + 16 i
+  const int a_row0 = wm * (16 * TM) + l16;  // + 16 i
   const int a_sw = swz_a<BK>(a_row0);  // unchanged by + 16 i
-  const int b_col0 = wn * 64 + l16;    // + 16 j
+  const int b_col0 = wn * (16 * TN) + l16;  // + 16 j
 
   f32x4 acc[TM][TN];
 #pragma unroll
@@ -214,9 +214,9 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
       if (t + s < nk) step(t + s, s);
   }
 
-  // ---- epilogue: lane holds C[m][n .. n+3], m = m0 + 64 wm + 16 i + l16,
-  // n = n0 + 64 wn + 16 j + 4 g
-  const int ncol = n0 + wn * 64 + 4 * g;
+  // ---- epilogue: lane holds C[m][n .. n+3], m = m0 + 16 TM wm + 16 i + l16,
+  // n = n0 + 16 TN wn + 16 j + 4 g
+  const int ncol = n0 + wn * (16 * TN) + 4 * g;
   if (args.partial == nullptr) {
     f32x4 bv[TN];
 #pragma unroll
@@ -224,7 +224,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
       bv[j] = args.bias ? *(const f32x4*)(args.bias + ncol + 16 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      float* row = args.C + (size_t)(m0 + wm * 64 + 16 * i + l16) * args.ldc;
+      float* row = args.C + (size_t)(m0 + wm * (16 * TM) + 16 * i + l16) * args.ldc;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         f32x4 v = acc[i][j] + bv[j];
@@ -240,7 +240,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
   float* plane = args.partial + (size_t)split * args.M * args.N;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    float* row = plane + (size_t)(m0 + wm * 64 + 16 * i + l16) * args.N;
+    float* row = plane + (size_t)(m0 + wm * (16 * TM) + 16 * i + l16) * args.N;
 #pragma unroll
     for (int j = 0; j < TN; ++j) splitk_store4(row + ncol + 16 * j, acc[i][j]);
   }

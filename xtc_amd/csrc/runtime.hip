@@ -454,7 +454,8 @@ bool skinny_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, in
 }
 
 // The LDS-DMA fp32 kernel (gemm_f32_lds.hpp) implements the 128x256x32 (2x4
-// waves) and 256x128x32 (4x2 waves) fp32 tiles, split-K included, when the
+// waves), 256x128x32 (4x2 waves) and 128x128x32 (2x4 waves) fp32 tiles,
+// split-K included, when the
 // shape needs no bounds checks: one workgroup of 8 waves per CU.
 bool f32_lds_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
                           int ldb, int ldc, const void* A, const void* B, const void* C,
@@ -466,7 +467,8 @@ bool f32_lds_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
   if (disabled || d.dtype != XTC_HIP_F32) return false;
   const bool t1 = t.bm == 128 && t.bn == 256 && t.wgm == 2 && t.wgn == 4;
   const bool t2 = t.bm == 256 && t.bn == 128 && t.wgm == 4 && t.wgn == 2;
-  if (!(t1 || t2) || t.bk != 32) return false;
+  const bool t3 = t.bm == 128 && t.bn == 128 && t.wgm == 2 && t.wgn == 4;
+  if (!(t1 || t2 || t3) || t.bk != 32) return false;
   const int splits = split_k < 1 ? 1 : split_k;
   if (d.M % t.bm || d.N % t.bn || d.K % (32 * splits)) return false;
   if (lda % 4 || ldb % 4 || ldc % 4) return false;
@@ -954,7 +956,9 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
     // same tiles, split-K set-up and grid as the generic instance; only the
     // kernel differs
     lds_entry = *e;
-    lds_entry.launch = t.wgm == 2 ? &launch_f32_lds<128, 256, 2, 4> : &launch_f32_lds<256, 128, 4, 2>;
+    lds_entry.launch = t.wgm == 4    ? &launch_f32_lds<256, 128, 4, 2>
+                       : t.bn == 256 ? &launch_f32_lds<128, 256, 2, 4>
+                                     : &launch_f32_lds<128, 128, 2, 4>;
     e = &lds_entry;
   }
   GemmArgs a;
