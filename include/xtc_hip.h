@@ -65,6 +65,17 @@ void *xtc_hip_stream(void);
 /* Waits for all work on the library stream (mgpuStreamSynchronize). */
 int xtc_hip_synchronize(void);
 
+/* A caller-owned stream of default priority on the current device
+ * (mgpuStreamCreate, GPUDevice.py:54-62), for the descriptors' `stream`
+ * field; waiting on one (mgpuStreamSynchronize, GPUDevice.py:171-178,
+ * NULL = the library stream); destroying one after its work is done, which
+ * also frees its scratch.  Split-K partial sums and counters and the
+ * staging copies of transposed operands are kept per stream, so calls on
+ * different streams may overlap; calls on one stream run in order. */
+void *xtc_hip_stream_create(void);
+int xtc_hip_stream_synchronize(void *stream);
+int xtc_hip_stream_destroy(void *stream);
+
 /* Device memory (mgpuMemAlloc / mgpuMemFree). NULL on failure. */
 void *xtc_hip_malloc(uint64_t bytes);
 int xtc_hip_free(void *ptr);

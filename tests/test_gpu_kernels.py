@@ -197,6 +197,42 @@ def test_split_k_conv_in_kernel_reduction():
         np.testing.assert_array_equal(out, expect)
 
 
+def test_split_k_on_concurrent_streams():
+    # Split-K partials, arrival counters and transposed-operand staging are
+    # kept per stream: split-K launches (generic, skinny bf16, with a
+    # transposed B staged first) queued on three streams without a wait in
+    # between must each come out exact.
+    L = capi.lib()
+    streams = [None, L.xtc_hip_stream_create(), L.xtc_hip_stream_create()]
+    assert streams[1] and streams[2], capi.last_error()
+    cases = [("float32", 256, 256, 8192, 8, 0), ("bfloat16", 16, 1024, 8192, 8, 0), ("float32", 128, 256, 4096, 4, 1)]
+    try:
+        jobs = []
+        for rep in range(3):
+            for si, s in enumerate(streams):
+                dtype, M, N, K, split, tb = cases[(si + rep) % 3]
+                a, b = _int_operands(M, N, K, 3 * rep + si)
+                A = _dev(a, dtype)
+                B = _dev(np.ascontiguousarray(b.T) if tb else b, dtype)
+                C = DeviceBuffer(M * N * 4)
+                d = capi.MatmulDesc()
+                d.dtype = capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16
+                d.M, d.N, d.K = M, N, K
+                d.split_k = split
+                d.xcd_remap = 1
+                d.trans_b = tb
+                d.stream = s
+                capi.check(L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, None), "matmul")
+                jobs.append((A, B, C, ref.matmul(a, b).astype(np.float32), f"rep {rep} stream {si} {dtype} {(M, N, K)}"))
+        for s in streams:
+            capi.check(L.xtc_hip_stream_synchronize(s), "stream sync")
+        for _, _, C, expect, what in jobs:
+            np.testing.assert_array_equal(C.to_numpy(expect.shape, np.float32), expect, err_msg=what)
+    finally:
+        for s in streams[1:]:
+            capi.check(L.xtc_hip_stream_destroy(s), "stream destroy")
+
+
 def test_matmul_relu_threshold_nan():
     a = np.ones((16, 8), np.float32)
     b = np.ones((8, 16), np.float32)

@@ -12,6 +12,7 @@
 
 #include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "gemm_bf16_lds.hpp"
 #include "gemm_bf16_skinny.hpp"
@@ -47,15 +48,23 @@ int fail(const char* fmt, ...) {
 
 constexpr int kMaxDevices = 16;
 
+// Scratch memory of one stream: split-K partial sums and arrival counters
+// (zero between launches), and natural copies of transposed operands.  Each
+// stream has its own, so launches on different streams never share scratch
+// and may overlap; launches on one stream are ordered by the stream.
+struct StreamScratch {
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  unsigned* counters = nullptr;
+  size_t counters_len = 0;
+  void* staging[2] = {nullptr, nullptr};
+  size_t staging_bytes[2] = {0, 0};
+};
+
 struct DeviceState {
   bool ready = false;
   hipStream_t stream = nullptr;
-  void* workspace = nullptr;   // split-K partial sums
-  size_t workspace_bytes = 0;
-  unsigned* counters = nullptr;  // split-K arrival counters (zero between launches)
-  size_t counters_len = 0;
-  void* staging[2] = {nullptr, nullptr};  // natural copies of transposed operands
-  size_t staging_bytes[2] = {0, 0};
+  std::unordered_map<hipStream_t, StreamScratch> scratch;  // by launch stream
   std::string arch, name;
 };
 
@@ -81,70 +90,68 @@ double now_s() {
   return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
 
-// Grows the per-device split-K workspace.  Returns null on failure.
-void* workspace(size_t bytes) {
+// Scratch of stream `s` on the current device, or null.  The caller holds
+// g_mutex.
+StreamScratch* stream_scratch(hipStream_t s) {
   DeviceState* d = current_state();
-  if (!d) return nullptr;
-  std::lock_guard<std::mutex> lk(g_mutex);
-  if (d->workspace_bytes < bytes) {
-    if (d->workspace) {
-      // launches on any stream (callers may pass their own) may still read it
-      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-      hipFree(d->workspace);
-      d->workspace = nullptr;
-      d->workspace_bytes = 0;
-    }
-    if (hipMalloc(&d->workspace, bytes) != hipSuccess) return nullptr;
-    d->workspace_bytes = bytes;
-  }
-  return d->workspace;
+  return d ? &d->scratch[s] : nullptr;
 }
 
-// Grows staging buffer `slot` (0: A, 1: B) of the current device.  Returns
-// null on failure.
-void* staging(int slot, size_t bytes) {
-  DeviceState* d = current_state();
-  if (!d) return nullptr;
-  std::lock_guard<std::mutex> lk(g_mutex);
-  if (d->staging_bytes[slot] < bytes) {
-    if (d->staging[slot]) {
-      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-      hipFree(d->staging[slot]);
-      d->staging[slot] = nullptr;
-      d->staging_bytes[slot] = 0;
-    }
-    if (hipMalloc(&d->staging[slot], bytes) != hipSuccess) return nullptr;
-    d->staging_bytes[slot] = bytes;
+// Replaces *buf by a buffer of `bytes` after the launches of stream `s` that
+// may still use the old one are done.  False on failure.
+bool regrow(void** buf, size_t* have, size_t bytes, hipStream_t s) {
+  if (*buf) {
+    if (hipStreamSynchronize(s) != hipSuccess) return false;
+    hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
   }
-  return d->staging[slot];
+  if (hipMalloc(buf, bytes) != hipSuccess) return false;
+  *have = bytes;
+  return true;
 }
 
-// Grows the per-device split-K arrival counters (splitk.hpp) to at least n
-// entries.  New counters are cleared here, once; every split-K launch leaves
-// them at zero.  Returns null on failure.
-unsigned* split_counters(size_t n) {
-  DeviceState* d = current_state();
-  if (!d) return nullptr;
+// Grows the split-K workspace of stream `s`.  Returns null on failure.
+void* workspace(size_t bytes, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mutex);
-  if (d->counters_len < n) {
+  StreamScratch* x = stream_scratch(s);
+  if (!x) return nullptr;
+  if (x->workspace_bytes < bytes && !regrow(&x->workspace, &x->workspace_bytes, bytes, s)) return nullptr;
+  return x->workspace;
+}
+
+// Grows staging buffer `slot` (0: A, 1: B) of stream `s`.  Returns null on
+// failure.
+void* staging(int slot, size_t bytes, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_mutex);
+  StreamScratch* x = stream_scratch(s);
+  if (!x) return nullptr;
+  if (x->staging_bytes[slot] < bytes && !regrow(&x->staging[slot], &x->staging_bytes[slot], bytes, s))
+    return nullptr;
+  return x->staging[slot];
+}
+
+// Grows the split-K arrival counters (splitk.hpp) of stream `s` to at least
+// n entries.  New counters are cleared here, once, on `s`; every split-K
+// launch leaves them at zero.  Returns null on failure.
+unsigned* split_counters(size_t n, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_mutex);
+  StreamScratch* x = stream_scratch(s);
+  if (!x) return nullptr;
+  if (x->counters_len < n) {
     const size_t len = n < 4096 ? 4096 : n;
-    if (d->counters) {
-      if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-      hipFree(d->counters);
-      d->counters = nullptr;
-      d->counters_len = 0;
-    }
-    unsigned* p = nullptr;
-    if (hipMalloc((void**)&p, len * sizeof(unsigned)) != hipSuccess) return nullptr;
-    if (hipMemsetAsync(p, 0, len * sizeof(unsigned), d->stream) != hipSuccess ||
-        hipStreamSynchronize(d->stream) != hipSuccess) {
-      hipFree(p);
+    size_t bytes = 0;
+    void* p = x->counters;
+    if (!regrow(&p, &bytes, len * sizeof(unsigned), s)) {
+      x->counters = nullptr;
+      x->counters_len = 0;
       return nullptr;
     }
-    d->counters = p;
-    d->counters_len = len;
+    x->counters = (unsigned*)p;
+    x->counters_len = len;
+    if (hipMemsetAsync(p, 0, bytes, s) != hipSuccess) return nullptr;
   }
-  return d->counters;
+  return x->counters;
 }
 
 // ------------------------------------------------------------ aux kernels
@@ -390,9 +397,9 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
   a.counters = nullptr;
   if (splits > 1) {
     size_t bytes = (size_t)splits * a.M * a.N * sizeof(float);
-    a.partial = (float*)workspace(bytes);
+    a.partial = (float*)workspace(bytes, s);
     if (!a.partial) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
-    a.counters = split_counters((size_t)a.tiles_m * a.tiles_n);
+    a.counters = split_counters((size_t)a.tiles_m * a.tiles_n, s);
     if (!a.counters) return fail("cannot allocate %d split-K counters", a.tiles_m * a.tiles_n);
   }
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
@@ -564,10 +571,10 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
     a.ldw = ldc;
   } else {
     size_t bytes = (size_t)splits * 16 * d.N * sizeof(float);
-    a.W = (float*)workspace(bytes);
+    a.W = (float*)workspace(bytes, s);
     if (!a.W) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
     a.ldw = d.N;
-    a.counters = split_counters((size_t)a.nblocks);
+    a.counters = split_counters((size_t)a.nblocks, s);
     if (!a.counters) return fail("cannot allocate %d split-K counters", a.nblocks);
   }
   dim3 grid((unsigned)(a.nblocks * splits));
@@ -698,7 +705,7 @@ __global__ void __launch_bounds__(256) transpose_kernel(const T* __restrict__ sr
 // staging buffer `slot`; null on failure (g_last_error set).
 const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src, int elem_bytes, hipStream_t s) {
   const size_t bytes = (size_t)R * Cc * elem_bytes;
-  void* dst = staging(slot, bytes);
+  void* dst = staging(slot, bytes, s);
   if (!dst) {
     fail("cannot allocate %zu bytes of transpose staging", bytes);
     return nullptr;
@@ -778,6 +785,47 @@ int xtc_hip_synchronize(void) {
   DeviceState* d = current_state();
   if (!d) return fail("xtc_hip_init not called");
   HIP_TRY(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+void* xtc_hip_stream_create(void) {
+  if (!current_state()) {
+    fail("xtc_hip_init not called");
+    return nullptr;
+  }
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+    fail("hipStreamCreateWithFlags failed");
+    return nullptr;
+  }
+  return (void*)s;
+}
+
+int xtc_hip_stream_synchronize(void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  HIP_TRY(hipStreamSynchronize(pick_stream(stream)));
+  return 0;
+}
+
+int xtc_hip_stream_destroy(void* stream) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  hipStream_t s = (hipStream_t)stream;
+  if (!s || s == d->stream) return fail("the library stream cannot be destroyed");
+  HIP_TRY(hipStreamSynchronize(s));
+  {
+    std::lock_guard<std::mutex> lk(g_mutex);
+    auto it = d->scratch.find(s);
+    if (it != d->scratch.end()) {
+      StreamScratch& x = it->second;
+      if (x.workspace) hipFree(x.workspace);
+      if (x.counters) hipFree(x.counters);
+      for (void* p : x.staging)
+        if (p) hipFree(p);
+      d->scratch.erase(it);
+    }
+  }
+  HIP_TRY(hipStreamDestroy(s));
   return 0;
 }
 

@@ -22,7 +22,8 @@
 // whole L2 of the XCD in every workgroup, which costs more than the reduce.
 // Counters start at zero (the host clears them once when it allocates them)
 // and every launch leaves them at zero.  Two launches that share the
-// counters and the workspace must not overlap (one stream per device).
+// counters and the workspace must not overlap: the host keeps both per
+// launch stream.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -124,6 +124,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "xtc_hip_device_name": (_i, [ctypes.c_char_p, _i]),
     "xtc_hip_stream": (_vp, []),
     "xtc_hip_synchronize": (_i, []),
+    "xtc_hip_stream_create": (_vp, []),
+    "xtc_hip_stream_synchronize": (_i, [_vp]),
+    "xtc_hip_stream_destroy": (_i, [_vp]),
     "xtc_hip_malloc": (_vp, [_u64]),
     "xtc_hip_free": (_i, [_vp]),
     "xtc_hip_memcpy_h2d": (_i, [_vp, _vp, _u64]),
