@@ -4,22 +4,25 @@
 // is one kernel (no second reduce launch, no launch gap).
 //
 // Protocol, per output tile with `splits` workgroups along K:
-//   1. every workgroup stores its fp32 partial tile to the workspace with
-//      agent-scope atomic stores (gfx950: global_store ... sc1, written
+//   1. every workgroup stores its fp32 partial tile to the workspace with the
+//      agent-scope cache policy (gfx950: global_store ... sc1, written
 //      through to the device coherence point, so the other XCDs' L2s never
-//      hold it dirty);
+//      hold it dirty): 16-byte stores where the tile allows, else the 4-byte
+//      agent-scope atomic store, which compiles to the same policy;
 //   2. every thread waits for its stores to complete (vmcnt(0)), the
 //      workgroup synchronises and one lane increments the tile's arrival
 //      counter (agent-scope atomic add);
 //   3. the workgroup that sees splits-1 is the last one: it reads the
-//      partials back with agent-scope atomic loads (global_load ... sc1),
-//      sums partial[0..splits-1] in split order (the result does not depend
-//      on which workgroup arrived last), applies bias / relu, stores C and
-//      sets the counter back to 0 for the next launch.
-// Every access to the published data is itself an agent-scope atomic, so no
+//      partials back with sc1 loads (16 bytes, or 4-byte agent-scope atomic
+//      loads), sums partial[0..splits-1] in split order (the result does not
+//      depend on which workgroup arrived last), applies bias / relu, stores C
+//      and sets the counter back to 0 for the next launch.
+// Every access to the published data carries the agent-scope policy, so no
 // L2 write-back (buffer_wbl2) or invalidate (buffer_inv) is needed: a
 // release/acquire fence at agent scope would write back and invalidate the
 // whole L2 of the XCD in every workgroup, which costs more than the reduce.
+// The 16-byte accesses halve the instructions of the 8-byte atomic pairs
+// they replaced and make the C5 MLP 4 % faster.
 // Counters start at zero (the host clears them once when it allocates them)
 // and every launch leaves them at zero.  Two launches that share the
 // counters and the workspace must not overlap: the host keeps both per
@@ -44,13 +47,13 @@ __device__ __forceinline__ float splitk_load(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16-byte aligned p: two 8-byte agent-scope stores / loads.
+// 16-byte aligned p: one 16-byte store with the agent-scope cache policy
+// (sc1, what an agent-scope atomic store of 8 bytes compiles to), issued from
+// asm because no atomic is 16 bytes wide; its completion is waited for in
+// splitk_arrive (s_waitcnt vmcnt(0)).  The s_nop covers the one wait state a
+// VALU write of the data registers needs after a store of more than 8 bytes.
 __device__ __forceinline__ void splitk_store4(float* p, splitk::f32x4 v) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(p);
-  const uint64_t lo = (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32);
-  const uint64_t hi = (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32);
-  __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
 }
 
 __device__ __forceinline__ splitk::f32x4 splitk_load4(const float* p) {
@@ -61,18 +64,63 @@ __device__ __forceinline__ splitk::f32x4 splitk_load4(const float* p) {
                        __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32))};
 }
 
-// sum_{s < splits} p[s * stride] in split order, 8 loads in flight.  A slot
-// past the last split adds +0.0, which leaves the sum unchanged: it starts at
-// +0.0 and so is never -0.0.
+// Loads of 16 bytes with the agent-scope cache policy (sc1), from asm; each
+// asm block waits for its own loads (s_waitcnt vmcnt(0)) before its outputs
+// are defined.
+#define XTC_SPLITK_LD(i, a) "global_load_dwordx4 %" #i ", %" #a ", off sc1\n\t"
+__device__ __forceinline__ void splitk_ld8(splitk::f32x4* t, const float* p, size_t stride) {
+  asm volatile(XTC_SPLITK_LD(0, 8) XTC_SPLITK_LD(1, 9) XTC_SPLITK_LD(2, 10) XTC_SPLITK_LD(3, 11)
+               XTC_SPLITK_LD(4, 12) XTC_SPLITK_LD(5, 13) XTC_SPLITK_LD(6, 14) XTC_SPLITK_LD(7, 15) "s_waitcnt vmcnt(0)"
+               : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]),
+                 "=&v"(t[7])
+               : "v"(p), "v"(p + stride), "v"(p + 2 * stride), "v"(p + 3 * stride), "v"(p + 4 * stride),
+                 "v"(p + 5 * stride), "v"(p + 6 * stride), "v"(p + 7 * stride)
+               : "memory");
+}
+__device__ __forceinline__ void splitk_ld4(splitk::f32x4* t, const float* p, size_t stride) {
+  asm volatile(XTC_SPLITK_LD(0, 4) XTC_SPLITK_LD(1, 5) XTC_SPLITK_LD(2, 6) XTC_SPLITK_LD(3, 7) "s_waitcnt vmcnt(0)"
+               : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
+               : "v"(p), "v"(p + stride), "v"(p + 2 * stride), "v"(p + 3 * stride)
+               : "memory");
+}
+__device__ __forceinline__ void splitk_ld2(splitk::f32x4* t, const float* p, size_t stride) {
+  asm volatile(XTC_SPLITK_LD(0, 2) XTC_SPLITK_LD(1, 3) "s_waitcnt vmcnt(0)"
+               : "=&v"(t[0]), "=&v"(t[1])
+               : "v"(p), "v"(p + stride)
+               : "memory");
+}
+__device__ __forceinline__ void splitk_ld1(splitk::f32x4* t, const float* p) {
+  asm volatile(XTC_SPLITK_LD(0, 1) "s_waitcnt vmcnt(0)" : "=&v"(t[0]) : "v"(p) : "memory");
+}
+#undef XTC_SPLITK_LD
+
+// sum_{s < splits} p[s * stride] in split order, starting from +0.0, up to 8
+// loads in flight.  Only the splits that exist are loaded: these loads go
+// past the L2.
 __device__ __forceinline__ splitk::f32x4 splitk_sum4(const float* p, size_t stride, int splits) {
-  constexpr int kBatch = 8;
   splitk::f32x4 v = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < splits; s0 += kBatch) {
-    splitk::f32x4 t[kBatch];
+  splitk::f32x4 t[8];
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    splitk_ld8(t, p + (size_t)s * stride, stride);
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) t[j] = splitk_load4(p + (size_t)min(s0 + j, splits - 1) * stride);
+    for (int j = 0; j < 8; ++j) v += t[j];
+  }
+  if (s + 4 <= splits) {
+    splitk_ld4(t, p + (size_t)s * stride, stride);
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) v += s0 + j < splits ? t[j] : splitk::f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) v += t[j];
+    s += 4;
+  }
+  if (s + 2 <= splits) {
+    splitk_ld2(t, p + (size_t)s * stride, stride);
+    v += t[0];
+    v += t[1];
+    s += 2;
+  }
+  if (s < splits) {
+    splitk_ld1(t, p + (size_t)s * stride);
+    v += t[0];
   }
   return v;
 }
@@ -83,9 +131,11 @@ __device__ __forceinline__ float splitk_sum1(const float* p, size_t stride, int 
   for (int s0 = 0; s0 < splits; s0 += kBatch) {
     float t[kBatch];
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) t[j] = splitk_load(p + (size_t)min(s0 + j, splits - 1) * stride);
+    for (int j = 0; j < kBatch; ++j)
+      if (s0 + j < splits) t[j] = splitk_load(p + (size_t)(s0 + j) * stride);
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) v += s0 + j < splits ? t[j] : 0.f;
+    for (int j = 0; j < kBatch; ++j)
+      if (s0 + j < splits) v += t[j];
   }
   return v;
 }
