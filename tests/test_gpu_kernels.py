@@ -532,16 +532,18 @@ def test_pingpong_bf16_transposed_b_matches_row_major_and_bk64():
     np.testing.assert_array_equal(out, same)
 
 
-# ------------------------------ LDS-DMA fp32 kernel (128x256x32 2x4, 256x128x32 4x2)
+# ------------- LDS-DMA fp32 kernel (BK 32: 128x256, 256x128, 128x128; BK 16: 128x256, 256x128)
 
-F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2), (128, 128, 32, 2, 4)]
+F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2), (128, 128, 32, 2, 4), (128, 256, 16, 2, 4), (256, 128, 16, 4, 2)]
 
 
 @pytest.mark.parametrize("tile", F32_LDS)
-@pytest.mark.parametrize("K,split", [(32, 1), (64, 1), (96, 1), (1024, 1), (1056, 1), (512, 2), (1024, 4), (2048, 8)])
+@pytest.mark.parametrize("K,split", [(16, 1), (32, 1), (64, 1), (80, 1), (96, 1), (1024, 1), (1056, 1), (512, 2),
+                                     (1024, 4), (2048, 8)])
 def test_f32_lds_integer_exact_every_pipeline_depth(tile, K, split):
-    # K / 32 / split slabs below, at and above the DMA lead (2); 2x2 or 2x4
-    # tiles; split-K finished in the kernel
+    # K / BK / split slabs below, at and above the DMA lead (2 for BK 32, 3
+    # or 4 for BK 16; K = 16 and 80 take the generic kernel at BK 32);
+    # split-K finished in the kernel
     M, N = 512, 512
     a, b = _int_operands(M, N, K, 7)
     out = run_matmul(a, b, "float32", tile=tile, split_k=split)

@@ -2,7 +2,7 @@
 // fp32 GEMM for aligned shapes on gfx950, LDS-DMA pipeline, one workgroup
 // of 8 waves per CU:
 //   C[M,N] = epilogue( A[M,K] @ B[K,N] ), fp32 row-major, optional split-K
-// with M % BM == 0, N % BN == 0, each split's K range a multiple of BK = 32,
+// with M % BM == 0, N % BN == 0, each split's K range a multiple of BK (16 or 32),
 // lda and ldb multiples of 4 and 16-byte aligned operands.
 //
 // v_mfma_f32_16x16x4_f32 issues at full rate with one or two waves per SIMD
@@ -94,14 +94,18 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_f32_
   static_assert(BK == 16 || BK == 32, "BK");
   static_assert(BN * 4 <= 1024 && 1024 % (BN * 4) == 0, "a DMA kilobyte holds whole B rows");
   static_assert(A_KB * 8 * 1024 == A_STAGE && B_KB * 8 * 1024 == B_STAGE, "stage must split over 8 waves");
-  static_assert(STAGES >= 2 && STAGES <= 4 && STAGES * STAGE <= 160 * 1024, "LDS");
+  static_assert(STAGES >= 2 && STAGES <= 6 && STAGES * STAGE <= 160 * 1024, "LDS");
   static_assert(D * DMA_PER_SLAB < 64, "vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char st2[STAGES > 2 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) unsigned char st3[STAGES > 3 ? STAGE : 16];
-  auto stage = [&](int s) -> unsigned char* { return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3; };
+  __shared__ __attribute__((aligned(1024))) unsigned char st4[STAGES > 4 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char st5[STAGES > 5 ? STAGE : 16];
+  auto stage = [&](int s) -> unsigned char* {
+    return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : s == 3 ? st3 : s == 4 ? st4 : st5;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
