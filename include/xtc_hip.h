@@ -76,6 +76,14 @@ void *xtc_hip_stream_create(void);
 int xtc_hip_stream_synchronize(void *stream);
 int xtc_hip_stream_destroy(void *stream);
 
+/* Frees the scratch the library holds for `stream` (split-K workspace and
+ * counters, transpose staging) once the stream's queued work is done,
+ * without destroying the stream: for streams the caller created itself and
+ * destroys with hipStreamDestroy.  A later call on the stream allocates its
+ * scratch again.  A stream's scratch is grown while the call that needs it
+ * is being queued, so one stream is driven by one host thread at a time. */
+int xtc_hip_stream_release(void *stream);
+
 /* Device memory (mgpuMemAlloc / mgpuMemFree). NULL on failure. */
 void *xtc_hip_malloc(uint64_t bytes);
 int xtc_hip_free(void *ptr);
@@ -134,6 +142,26 @@ typedef struct {
 
 int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B,
                    float *C, const float *bias);
+
+/* Per-device scratch of xtc_hip_matmul_noalloc: 64 MiB. */
+#define XTC_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* xtc_hip_matmul that allocates nothing (no hipMalloc/hipFree, no library
+ * allocation).  It has no counterpart in the reference: it is for callers
+ * that cannot allocate device memory, such as code under HIP graph capture,
+ * tight serving loops and harnesses that forbid allocation.  Same arguments,
+ * kernels and results as xtc_hip_matmul.  Its scratch -- split-K partial sums
+ * ([splits][M][N] fp32, or [splits][16][N] for the skinny kernel), one
+ * arrival counter per output tile, and dense copies of transposed operands
+ * that the kernels cannot read in place -- comes from one static array per
+ * device of XTC_HIP_NOALLOC_SCRATCH_BYTES, set up by xtc_hip_init.  A call
+ * that needs more fails with a message instead of launching its GEMM.  The
+ * counters are cleared by a kernel on the call's stream before the GEMM.
+ * Every call on a device shares that device's array, whatever its stream:
+ * calls that overlap on one device race, so callers order them (one stream,
+ * or a wait between streams). */
+int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc *desc, const void *A,
+                           const void *B, float *C, const float *bias);
 
 /* O[b,oh,ow,f] = relu?( sum_{r,s,c} Ipad[b,oh*sh+r,ow*sw+s,c] * W[r,s,c,f] )
  * NHWC x RSCF -> NHWC (XTCOperConv2D, operators.py:252-347;

@@ -25,6 +25,12 @@
 
 using namespace xtc_hip;
 
+// Scratch memory of xtc_hip_matmul_noalloc: one copy per device, for the
+// whole life of the process.  Host code never uses this name as an address
+// (in host code it is only a stand-in for the device symbol): xtc_hip_init
+// looks up each device's address of it once (DeviceState::scratch_ptr).
+static __device__ __align__(256) unsigned char scratch[XTC_HIP_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -64,6 +70,7 @@ struct StreamScratch {
 struct DeviceState {
   bool ready = false;
   hipStream_t stream = nullptr;
+  void* scratch_ptr = nullptr;  // this device's address of `scratch`
   std::unordered_map<hipStream_t, StreamScratch> scratch;  // by launch stream
   std::string arch, name;
 };
@@ -131,28 +138,84 @@ void* staging(int slot, size_t bytes, hipStream_t s) {
   return x->staging[slot];
 }
 
+bool zero_fill(void* p, size_t bytes, hipStream_t s);
+
 // Grows the split-K arrival counters (splitk.hpp) of stream `s` to at least
-// n entries.  New counters are cleared here, once, on `s`; every split-K
-// launch leaves them at zero.  Returns null on failure.
+// n entries.  New counters are cleared here, once, on `s` (by a kernel, not
+// a memset node, so the call may be captured in a graph); every split-K
+// launch leaves them at zero.  The stream's record is only updated once the
+// clear is queued.  Returns null on failure.
 unsigned* split_counters(size_t n, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mutex);
   StreamScratch* x = stream_scratch(s);
   if (!x) return nullptr;
   if (x->counters_len < n) {
     const size_t len = n < 4096 ? 4096 : n;
-    size_t bytes = 0;
+    size_t bytes = x->counters_len * sizeof(unsigned);
     void* p = x->counters;
-    if (!regrow(&p, &bytes, len * sizeof(unsigned), s)) {
-      x->counters = nullptr;
-      x->counters_len = 0;
+    x->counters = nullptr;  // regrow frees the old array first
+    x->counters_len = 0;
+    if (!regrow(&p, &bytes, len * sizeof(unsigned), s)) return nullptr;
+    if (!zero_fill(p, bytes, s)) {
+      hipFree(p);
       return nullptr;
     }
     x->counters = (unsigned*)p;
     x->counters_len = len;
-    if (hipMemsetAsync(p, 0, bytes, s) != hipSuccess) return nullptr;
   }
   return x->counters;
 }
+
+// Where one call takes its scratch memory from (split-K partial sums and
+// arrival counters, natural copies of transposed operands).
+//  * Growing mode (`fixed` null, xtc_hip_matmul and xtc_hip_conv2d): the
+//    per-stream buffers above, allocated or enlarged on demand.
+//  * Fixed mode (xtc_hip_matmul_noalloc): consecutive 256-byte aligned pieces
+//    of the device's static `scratch` array, at most `cap` bytes in all;
+//    nothing is allocated, and the counters are cleared by a kernel on the
+//    call's stream before the launch that uses them.
+struct Scratch {
+  hipStream_t s;
+  char* fixed = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+
+  void* take(size_t bytes, const char* what) {
+    const size_t off = (used + 255) & ~(size_t)255;
+    if (off > cap || bytes > cap - off) {
+      fail("xtc_hip_matmul_noalloc: %s need %zu bytes at offset %zu of the %zu-byte scratch", what, bytes, off,
+           cap);
+      return nullptr;
+    }
+    used = off + bytes;
+    return fixed + off;
+  }
+  float* partials(size_t bytes) {
+    if (fixed) return (float*)take(bytes, "split-K partial sums");
+    void* p = workspace(bytes, s);
+    if (!p) fail("cannot allocate %zu bytes of split-K workspace", bytes);
+    return (float*)p;
+  }
+  unsigned* counters(size_t n) {
+    if (fixed) {
+      unsigned* p = (unsigned*)take(n * sizeof(unsigned), "split-K counters");
+      if (p && !zero_fill(p, n * sizeof(unsigned), s)) {
+        fail("cannot clear %zu split-K counters", n);
+        return nullptr;
+      }
+      return p;
+    }
+    unsigned* p = split_counters(n, s);
+    if (!p) fail("cannot allocate %zu split-K counters", n);
+    return p;
+  }
+  void* stage(int slot, size_t bytes) {
+    if (fixed) return take(bytes, "transposed operand copies");
+    void* p = staging(slot, bytes, s);
+    if (!p) fail("cannot allocate %zu bytes of transpose staging", bytes);
+    return p;
+  }
+};
 
 // ------------------------------------------------------------ aux kernels
 
@@ -161,6 +224,17 @@ __global__ void fill_zero_kernel(uint4* p, uint64_t n16, unsigned char* tail, in
   uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (; i < n16; i += stride) p[i] = make_uint4(0, 0, 0, 0);
   if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
+int grid_for(uint64_t n, int block);
+
+// Queues a zero fill of `bytes` at 16-byte aligned p on `s`.
+bool zero_fill(void* p, size_t bytes, hipStream_t s) {
+  const uint64_t n16 = bytes / 16;
+  const int ntail = (int)(bytes % 16);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n16 ? n16 : 1, 256)), dim3(256), 0, s, (uint4*)p, n16,
+                     (unsigned char*)p + n16 * 16, ntail);
+  return hipGetLastError() == hipSuccess;
 }
 
 __global__ void relu_kernel(const float* __restrict__ x, float* __restrict__ y, uint64_t n,
@@ -383,7 +457,8 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
 }
 
 int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m, int xcd_remap,
-                       hipStream_t s) {
+                       Scratch& x) {
+  const hipStream_t s = x.s;
   a.tiles_m = (a.M + e->bm - 1) / e->bm;
   a.tiles_n = (a.N + e->bn - 1) / e->bn;
   a.group_m = group_m > 0 ? group_m : 8;
@@ -397,10 +472,10 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
   a.counters = nullptr;
   if (splits > 1) {
     size_t bytes = (size_t)splits * a.M * a.N * sizeof(float);
-    a.partial = (float*)workspace(bytes, s);
-    if (!a.partial) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
-    a.counters = split_counters((size_t)a.tiles_m * a.tiles_n, s);
-    if (!a.counters) return fail("cannot allocate %d split-K counters", a.tiles_m * a.tiles_n);
+    a.partial = x.partials(bytes);
+    if (!a.partial) return 1;
+    a.counters = x.counters((size_t)a.tiles_m * a.tiles_n);
+    if (!a.counters) return 1;
   }
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
   e->launch(a, grid, s);
@@ -551,7 +626,8 @@ int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, in
 }
 
 int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
-                       const void* A, const void* B, float* C, const float* bias, hipStream_t s) {
+                       const void* A, const void* B, float* C, const float* bias, Scratch& x) {
+  const hipStream_t s = x.s;
   const int splits = split_k < 1 ? 1 : split_k;
   SkinnyArgs a;
   a.A = (const __bf16*)A;
@@ -573,11 +649,11 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
     a.ldw = ldc;
   } else {
     size_t bytes = (size_t)splits * 16 * d.N * sizeof(float);
-    a.W = (float*)workspace(bytes, s);
-    if (!a.W) return fail("cannot allocate %zu bytes of split-K workspace", bytes);
+    a.W = x.partials(bytes);
+    if (!a.W) return 1;
     a.ldw = d.N;
-    a.counters = split_counters((size_t)a.nblocks, s);
-    if (!a.counters) return fail("cannot allocate %d split-K counters", a.nblocks);
+    a.counters = x.counters((size_t)a.nblocks);
+    if (!a.counters) return 1;
   }
   dim3 grid((unsigned)(a.nblocks * splits));
   if (d.K / splits == 1024)
@@ -705,13 +781,11 @@ __global__ void __launch_bounds__(256) transpose_kernel(const T* __restrict__ sr
 
 // Dense [Cc][R] copy of the R x Cc matrix at src (row stride ld_src) in
 // staging buffer `slot`; null on failure (g_last_error set).
-const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src, int elem_bytes, hipStream_t s) {
+const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src, int elem_bytes, Scratch& x) {
+  const hipStream_t s = x.s;
   const size_t bytes = (size_t)R * Cc * elem_bytes;
-  void* dst = staging(slot, bytes, s);
-  if (!dst) {
-    fail("cannot allocate %zu bytes of transpose staging", bytes);
-    return nullptr;
-  }
+  void* dst = x.stage(slot, bytes);
+  if (!dst) return nullptr;
   dim3 grid((unsigned)((Cc + 63) / 64), (unsigned)((R + 63) / 64));
   if (grid.y > 65535u) {
     fail("transpose: %d rows exceed the grid limit", R);
@@ -727,6 +801,102 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
     return nullptr;
   }
   return dst;
+}
+
+// xtc_hip_matmul with its scratch taken from `x` (whose stream is the
+// descriptor's).
+int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, float* C, const float* bias,
+                Scratch& x) {
+  if (!A || !B || !C) return fail("null operand");
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+  int lda = d.lda ? d.lda : (ta ? d.M : d.K);
+  int ldb = d.ldb ? d.ldb : (tb ? d.K : d.N);
+  const int ldc = d.ldc ? d.ldc : d.N;
+  if (lda < (ta ? d.M : d.K) || ldb < (tb ? d.K : d.N) || ldc < d.N)
+    return fail("leading dimension smaller than shape");
+  const hipStream_t s = x.s;
+  xtc_hip_tile t = d.tile;
+  int split_k = d.split_k;
+  if (t.bm == 0) {
+    int sk = 1;
+    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
+    if (split_k <= 0) split_k = sk;
+  }
+  // B stored transposed feeds the LDS-DMA kernel directly (B^T tiles are
+  // read like A tiles); every other transposed operand gets a natural copy
+  // in a staging buffer first (one HBM-bound transpose).
+  if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true))
+    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, true);
+  const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
+  if (ta) {
+    A = transposed_copy(0, A, d.K, d.M, lda, esz, x);
+    if (!A) return 1;
+    lda = d.K;
+  }
+  if (tb) {
+    B = transposed_copy(1, B, d.N, d.K, ldb, esz, x);
+    if (!B) return 1;
+    ldb = d.N;
+  }
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 &&
+                      aligned16(A) && aligned16(B);
+  if (!vec_ok) {
+    dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
+    if (d.dtype == XTC_HIP_F32)
+      hipLaunchKernelGGL(gemm_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)A,
+                         (const float*)B, C, bias, d.M, d.N, d.K, lda, ldb, ldc, d.relu,
+                         d.relu_threshold);
+    else
+      hipLaunchKernelGGL(gemm_naive_kernel<uint16_t>, grid, dim3(128), 0, s,
+                         (const uint16_t*)A, (const uint16_t*)B, C, bias, d.M, d.N, d.K, lda,
+                         ldb, ldc, d.relu, d.relu_threshold);
+    HIP_TRY(hipGetLastError());
+    return 0;
+  }
+  const GemmEntry* e = find_entry(d.dtype, 0, t);
+  if (!e)
+    return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
+                t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, false))
+    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, false);
+  if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
+    return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, x);
+  if (splitwave_gemm_applies(d, t, split_k, lda, A))
+    return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
+  GemmEntry lds_entry;
+  if (f32_lds_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias)) {
+    // same tiles, split-K set-up and grid as the generic instance; only the
+    // kernel differs
+    lds_entry = *e;
+    // BK 16 stages are 24 KB: 4 of them (256x128) or 5 (128x256).  Against
+    // 3 stages of BK 32 they measured 2-4 % faster on one box and 1-1.5 %
+    // slower on another, bit-identical
+    if (t.bk == 16)
+      lds_entry.launch = t.wgm == 4 ? &launch_f32_lds<256, 128, 16, 4, 2, 4> : &launch_f32_lds<128, 256, 16, 2, 4, 5>;
+    else
+      lds_entry.launch = t.wgm == 4    ? &launch_f32_lds<256, 128, 32, 4, 2, 3>
+                         : t.bn == 256 ? &launch_f32_lds<128, 256, 32, 2, 4, 3>
+                                       : &launch_f32_lds<128, 128, 32, 2, 4, 3>;
+    e = &lds_entry;
+  }
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.bias = bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold;
+  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, x);
 }
 
 }  // namespace
@@ -752,6 +922,7 @@ int xtc_hip_init(int device) {
     HIP_TRY(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, device));
+    HIP_TRY(hipGetSymbolAddress(&d.scratch_ptr, HIP_SYMBOL(scratch)));
     d.arch = prop.gcnArchName;
     d.name = prop.name;
     d.ready = true;
@@ -814,20 +985,26 @@ int xtc_hip_stream_destroy(void* stream) {
   if (!d) return fail("xtc_hip_init not called");
   hipStream_t s = (hipStream_t)stream;
   if (!s || s == d->stream) return fail("the library stream cannot be destroyed");
-  HIP_TRY(hipStreamSynchronize(s));
-  {
-    std::lock_guard<std::mutex> lk(g_mutex);
-    auto it = d->scratch.find(s);
-    if (it != d->scratch.end()) {
-      StreamScratch& x = it->second;
-      if (x.workspace) hipFree(x.workspace);
-      if (x.counters) hipFree(x.counters);
-      for (void* p : x.staging)
-        if (p) hipFree(p);
-      d->scratch.erase(it);
-    }
-  }
+  if (xtc_hip_stream_release(stream)) return 1;
   HIP_TRY(hipStreamDestroy(s));
+  return 0;
+}
+
+int xtc_hip_stream_release(void* stream) {
+  DeviceState* d = current_state();
+  if (!d) return fail("xtc_hip_init not called");
+  hipStream_t s = pick_stream(stream);
+  HIP_TRY(hipStreamSynchronize(s));
+  std::lock_guard<std::mutex> lk(g_mutex);
+  auto it = d->scratch.find(s);
+  if (it != d->scratch.end()) {
+    StreamScratch& x = it->second;
+    if (x.workspace) hipFree(x.workspace);
+    if (x.counters) hipFree(x.counters);
+    for (void* p : x.staging)
+      if (p) hipFree(p);
+    d->scratch.erase(it);
+  }
   return 0;
 }
 
@@ -941,97 +1118,20 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B
                    const float* bias) {
   if (!desc) return fail("null descriptor");
   if (!current_state()) return fail("xtc_hip_init not called");
-  if (!A || !B || !C) return fail("null operand");
-  const xtc_hip_matmul_desc& d = *desc;
-  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
-  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
-  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
-  int lda = d.lda ? d.lda : (ta ? d.M : d.K);
-  int ldb = d.ldb ? d.ldb : (tb ? d.K : d.N);
-  const int ldc = d.ldc ? d.ldc : d.N;
-  if (lda < (ta ? d.M : d.K) || ldb < (tb ? d.K : d.N) || ldc < d.N)
-    return fail("leading dimension smaller than shape");
-  hipStream_t s = pick_stream(d.stream);
-  xtc_hip_tile t = d.tile;
-  int split_k = d.split_k;
-  if (t.bm == 0) {
-    int sk = 1;
-    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
-    if (split_k <= 0) split_k = sk;
-  }
-  // B stored transposed feeds the LDS-DMA kernel directly (B^T tiles are
-  // read like A tiles); every other transposed operand gets a natural copy
-  // in a staging buffer first (one HBM-bound transpose).
-  if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true))
-    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, true);
-  const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
-  if (ta) {
-    A = transposed_copy(0, A, d.K, d.M, lda, esz, s);
-    if (!A) return 1;
-    lda = d.K;
-  }
-  if (tb) {
-    B = transposed_copy(1, B, d.N, d.K, ldb, esz, s);
-    if (!B) return 1;
-    ldb = d.N;
-  }
-  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
-  const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 &&
-                      aligned16(A) && aligned16(B);
-  if (!vec_ok) {
-    dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
-    if (d.dtype == XTC_HIP_F32)
-      hipLaunchKernelGGL(gemm_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)A,
-                         (const float*)B, C, bias, d.M, d.N, d.K, lda, ldb, ldc, d.relu,
-                         d.relu_threshold);
-    else
-      hipLaunchKernelGGL(gemm_naive_kernel<uint16_t>, grid, dim3(128), 0, s,
-                         (const uint16_t*)A, (const uint16_t*)B, C, bias, d.M, d.N, d.K, lda,
-                         ldb, ldc, d.relu, d.relu_threshold);
-    HIP_TRY(hipGetLastError());
-    return 0;
-  }
-  const GemmEntry* e = find_entry(d.dtype, 0, t);
-  if (!e)
-    return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
-                t.bm, t.bn, t.bk, t.wgm, t.wgn);
-  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, false))
-    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, false);
-  if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
-    return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
-  if (splitwave_gemm_applies(d, t, split_k, lda, A))
-    return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
-  GemmEntry lds_entry;
-  if (f32_lds_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias)) {
-    // same tiles, split-K set-up and grid as the generic instance; only the
-    // kernel differs
-    lds_entry = *e;
-    // BK 16 stages are 24 KB: 4 of them (256x128) or 5 (128x256).  Against
-    // 3 stages of BK 32 they measured 2-4 % faster on one box and 1-1.5 %
-    // slower on another, bit-identical
-    if (t.bk == 16)
-      lds_entry.launch = t.wgm == 4 ? &launch_f32_lds<256, 128, 16, 4, 2, 4> : &launch_f32_lds<128, 256, 16, 2, 4, 5>;
-    else
-      lds_entry.launch = t.wgm == 4    ? &launch_f32_lds<256, 128, 32, 4, 2, 3>
-                         : t.bn == 256 ? &launch_f32_lds<128, 256, 32, 2, 4, 3>
-                                       : &launch_f32_lds<128, 128, 32, 2, 4, 3>;
-    e = &lds_entry;
-  }
-  GemmArgs a;
-  memset(&a, 0, sizeof(a));
-  a.A = A;
-  a.B = B;
-  a.C = C;
-  a.bias = bias;
-  a.M = d.M;
-  a.N = d.N;
-  a.K = d.K;
-  a.lda = lda;
-  a.ldb = ldb;
-  a.ldc = ldc;
-  a.relu = d.relu;
-  a.relu_threshold = d.relu_threshold;
-  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, s);
+  Scratch x{pick_stream(desc->stream)};
+  return matmul_impl(*desc, A, B, C, bias, x);
+}
+
+int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc* desc, const void* A, const void* B, float* C,
+                           const float* bias) {
+  if (!desc) return fail("null descriptor");
+  DeviceState* dev = current_state();
+  if (!dev) return fail("xtc_hip_init not called");
+  if (!dev->scratch_ptr) return fail("xtc_hip_matmul_noalloc: no scratch address for this device");
+  Scratch x{pick_stream(desc->stream)};
+  x.fixed = (char*)dev->scratch_ptr;
+  x.cap = XTC_HIP_NOALLOC_SCRATCH_BYTES;
+  return matmul_impl(*desc, A, B, C, bias, x);
 }
 
 int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const void* weight,
@@ -1108,7 +1208,8 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   a.cPH = d.pad_top;
   a.cPW = d.pad_left;
   a.pad_value = d.pad_value;
-  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, s);
+  Scratch x{s};
+  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, x);
 }
 
 int xtc_hip_relu(const float* x, float* y, uint64_t n, float threshold, void* stream) {

@@ -127,6 +127,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "xtc_hip_stream_create": (_vp, []),
     "xtc_hip_stream_synchronize": (_i, [_vp]),
     "xtc_hip_stream_destroy": (_i, [_vp]),
+    "xtc_hip_stream_release": (_i, [_vp]),
     "xtc_hip_malloc": (_vp, [_u64]),
     "xtc_hip_free": (_i, [_vp]),
     "xtc_hip_memcpy_h2d": (_i, [_vp, _vp, _u64]),
@@ -138,6 +139,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "xtc_hip_event_elapsed_ms": (_i, [_vp, _vp, ctypes.POINTER(_f)]),
     "xtc_hip_event_destroy": (_i, [_vp]),
     "xtc_hip_matmul": (_i, [ctypes.POINTER(MatmulDesc), _vp, _vp, _vp, _vp]),
+    "xtc_hip_matmul_noalloc": (_i, [ctypes.POINTER(MatmulDesc), _vp, _vp, _vp, _vp]),
     "xtc_hip_conv2d": (_i, [ctypes.POINTER(Conv2dDesc), _vp, _vp, _vp, _vp]),
     "xtc_hip_relu": (_i, [_vp, _vp, _u64, _f, _vp]),
     "xtc_hip_pad": (
