@@ -40,105 +40,7 @@ PEAK_TFLOPS = {"bfloat16": 2516.6, "float32": 157.3}  # dense MFMA, MI355X datas
 PEAK_HBM_GBS = 8000.0
 
 
-def _graph(cfg: str):  # type: ignore[no-untyped-def]
-    import xtc_amd.graphs.xtc.op as O
-
-    if cfg == "C3a":
-        a = O.tensor((8192, 8192), "bfloat16", name="A")
-        b = O.tensor((8192, 8192), "bfloat16", name="B")
-        with O.graph(name="matmul_bf16") as gb:
-            O.matmul(a, b, name="C", out_dtype="float32")
-    elif cfg == "C3b":
-        a = O.tensor((16, 8192), "bfloat16", name="A")
-        b = O.tensor((8192, 8192), "bfloat16", name="B")
-        with O.graph(name="matmul_skinny") as gb:
-            O.matmul(a, b, name="C", out_dtype="float32")
-    elif cfg in ("C1", "C2"):
-        n = 512 if cfg == "C1" else 4096
-        a = O.tensor((n, n), "float32", name="A")
-        b = O.tensor((n, n), "float32", name="B")
-        with O.graph(name="matmul") as gb:
-            O.matmul(a, b, name="C")
-    elif cfg == "C4":
-        x = O.tensor((8, 56, 56, 64), "float32", name="I")
-        w = O.tensor((3, 3, 64, 64), "float32", name="W")
-        with O.graph(name="conv_relu") as gb:
-            p = O.pad2d(x, padding=1, axes=(1, 2), name="pad")
-            c = O.conv2d(p, w, name="conv")
-            O.relu(c, name="relu")
-    elif cfg == "C5":
-        x = O.tensor((2048, 1024), "float32", name="X")
-        w1 = O.tensor((1024, 4096), "float32", name="W1")
-        w2 = O.tensor((4096, 1024), "float32", name="W2")
-        with O.graph(name="mlp") as gb:
-            h = O.relu(O.matmul(x, w1, name="fc1"), name="act")
-            O.matmul(h, w2, name="fc2")
-    else:
-        raise SystemExit(f"unknown config {cfg}")
-    return gb.graph
-
-
-# Tuned schedules, expressed with XTC's scheduling primitives: the first tile
-# level of i/j is the workgroup tile, the second the wave tile, k's first
-# level the LDS slab; parallelize on k splits K (its first level is then the
-# slice per split, its second the slab) (xtc_amd/backends/hip/mapping.py).
-# Picked with loop-explore --strategy tile_hip on MI355X; nodes without an
-# entry keep the library's default tile.
-SCHEDULES = {
-    "C3a": {"C": {"tile": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}}},
-    "C2": {"C": {"tile": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 32}}}},
-    "C1": {"C": {"tile": {"i": {"i1": 32, "i2": 32}, "j": {"j1": 32, "j2": 32}, "k": {"k1": 128, "k2": 16}},
-                 "parallelize": ["i", "j", "k"]}},
-    "C5": {
-        "fc1": {"tile": {"i": {"i1": 128, "i2": 64}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}},
-        "fc2": {"tile": {"i": {"i1": 128, "i2": 64}, "j": {"j1": 128, "j2": 32}, "k": {"k1": 2048, "k2": 32}},
-                "parallelize": ["i", "j", "k"]},
-    },
-}
-
-
-def _inputs(cfg: str, graph) -> list[np.ndarray]:  # type: ignore[no-untyped-def]
-    """Seeded inputs of the BASELINE configuration: one default_rng(0), drawn
-    in graph input order in float64, cast (bf16: rounded)."""
-    from xtc_amd.utils.bf16 import round_to_bf16
-
-    rng = np.random.default_rng(0)
-    out = []
-    for t in graph.inputs_types:
-        shape = tuple(t.constant_shape)
-        if cfg == "C4" and len(shape) == 4 and shape[0] == 3:
-            arr = rng.normal(0.0, np.sqrt(2.0 / (9 * 64)), size=shape)
-        elif cfg == "C4":
-            arr = rng.uniform(0.0, 1.0, size=shape)
-        elif cfg == "C5" and shape != (2048, 1024):
-            arr = rng.normal(0.0, 0.02, size=shape)
-        else:
-            arr = rng.uniform(-1.0, 1.0, size=shape)
-        arr = arr.astype(np.float32)
-        out.append(round_to_bf16(arr) if t.constant_dtype == "bfloat16" else arr)
-    return out
-
-
-def _flops(cfg: str) -> int:
-    return {
-        "C1": 2 * 512**3,
-        "C2": 2 * 4096**3,
-        "C3a": 2 * 8192**3,
-        "C3b": 2 * 16 * 8192 * 8192,
-        "C4": 2 * 8 * 56 * 56 * 64 * 576,
-        "C5": 2 * 2048 * 4096 * 1024 * 2,
-    }[cfg]
-
-
-def _alg_bytes(cfg: str) -> int:
-    return {
-        "C1": 3 * 512 * 512 * 4,
-        "C2": 3 * 4096 * 4096 * 4,
-        "C3a": 2 * 8192 * 8192 * 2 + 8192 * 8192 * 4,
-        "C3b": 16 * 8192 * 2 + 8192 * 8192 * 2 + 16 * 8192 * 4,
-        "C4": 8 * 56 * 56 * 64 * 4 * 2 + 9 * 64 * 64 * 4,
-        "C5": (2048 * 1024 + 1024 * 4096 + 2 * 2048 * 4096 + 4096 * 1024 + 2048 * 1024) * 4,
-    }[cfg]
+from xtc_amd import configs as workloads  # noqa: E402  (graphs, seeded inputs, tuned schedules)
 
 
 def _traffic(cfg: str) -> float | None:
@@ -225,7 +127,7 @@ def _xtc_protocol(cfg: str, backend, sch, dev, cargs, flops: int, dtype: str) ->
         proto[f"{label}_median_ms"] = round(statistics.median(vals) * 1e3, 4)
     if status():
         raise SystemExit("payload reported an error under the evaluate_perf protocol")
-    rate = (_alg_bytes(cfg) / (proto["device_min_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS if cfg == "C3b"
+    rate = (workloads.alg_bytes(cfg) / (proto["device_min_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS if cfg == "C3b"
             else flops / (proto["device_min_ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[dtype])
     proto["device_min_pct_of_peak"] = round(100 * rate, 2)
     return proto
@@ -292,15 +194,9 @@ def main(argv: list[str] | None = None) -> int:
     from xtc_amd.runtimes.hip.ndarray import DeviceArray
 
     cfg = args.config
-    graph = _graph(cfg)
+    graph = workloads.graph(cfg)
     backend = Backend(graph)
-    sch = backend.get_scheduler()
-    for node, spec in SCHEDULES.get(cfg, {}).items():
-        node_sch = sch.for_node(node)
-        for dim, tiles in spec["tile"].items():
-            node_sch.tile(dim, tiles)
-        if "parallelize" in spec:
-            node_sch.parallelize(spec["parallelize"])
+    sch = workloads.apply_schedule(backend.get_scheduler(), cfg)
     module = backend.get_compiler(synchronize=False, schedule_policy="strict").compile(sch.schedule())
 
     dev = HipDevice(0)
@@ -311,7 +207,7 @@ def main(argv: list[str] | None = None) -> int:
     status = dev.module_symbol(module, f"{module.payload_name}_status")
     status.restype = ctypes.c_int
 
-    host_in = _inputs(cfg, graph)
+    host_in = workloads.inputs(cfg, graph)
     d_in = [DeviceArray.from_numpy(a, t.constant_dtype, dev) for a, t in zip(host_in, graph.inputs_types)]
     d_out = [DeviceArray(t.constant_shape, t.constant_dtype, dev) for t in graph.outputs_types]
     cargs = [ctypes.c_void_p(d.data) for d in (*d_in, *d_out)]
@@ -354,11 +250,11 @@ def main(argv: list[str] | None = None) -> int:
         raise SystemExit("payload reported an error during the timed region")
     kernel_s = ms.value * 1e-3 / args.steps
     step_s = wall / args.steps
-    flops = _flops(cfg)
+    flops = workloads.flops(cfg)
     dtype = graph.inputs_types[0].constant_dtype
     kernels = "; ".join(f"{n}: {c.describe()}" for n, c in module.configs.items()) or None
     if cfg == "C3b":
-        achieved = _alg_bytes(cfg) / kernel_s / 1e9
+        achieved = workloads.alg_bytes(cfg) / kernel_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     else:
         achieved = flops / kernel_s / 1e12

@@ -226,13 +226,28 @@ int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile 
 /* Same protocol as evaluate_perf (evaluate_perf.c:63-125): one warm-up call
  * when number > 0, then for each of `repeat` repeats the call count doubles
  * from `number` until a batch lasts >= min_repeat_ms; results[r] = batch
- * seconds / calls.  With events: "gpu.time" gives device seconds per call
- * measured by events bracketing the batch on the library stream;
- * "gpu.clocks" the same in nanoseconds.  Unknown events yield -1.  func is
- * called with nargs (<= 8) pointer arguments. */
+ * seconds / calls.  With events, results[r * events_num + e] is event e's
+ * count for the final batch of repeat r divided by its calls:
+ *   "gpu.time"   device seconds, from events bracketing the batch on the
+ *                library stream; "gpu.clocks" the same in nanoseconds;
+ *   "gpu.<name>" a GPU hardware counter through libxtc_hip_pmu.so
+ *                (include/xtc_hip_pmu.h; "gpu.cycles" = GRBM_GUI_ACTIVE),
+ *                as perf_event_gpu.cpp:56-233 reads CUPTI metrics;
+ *   "cycles", "clocks", "instructions", "migrations", "context_switches",
+ *   "cache_access", "cache_misses", "branches", "branches_misses"
+ *                host counters of the calling process through
+ *                perf_event_open (perf_event_linux.c:37-54,72-81).
+ * A name that cannot be opened yields -1, as in the reference.  At most 64
+ * events; func is called with nargs (<= 8) pointer arguments. */
 void xtc_hip_evaluate_perf(double *results, int events_num, const char *events_names[],
                            int repeat, int number, int min_repeat_ms,
                            void (*func)(void), void **args, int nargs);
+
+/* Status of the calling thread's last xtc_hip_evaluate_perf / evaluate:
+ * 0 when it ran, non-zero when it rejected its arguments (message in
+ * xtc_hip_last_error()).  The reference's evaluate_perf returns nothing and
+ * asserts instead. */
+int xtc_hip_evaluate_status(void);
 
 /* evaluate_perf without events (evaluate_perf.c:240-248). */
 void xtc_hip_evaluate(double *results, int repeat, int number, int min_repeat_ms,

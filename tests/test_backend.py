@@ -11,6 +11,7 @@ import subprocess
 import threading
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 import xtc_amd.graphs.xtc.op as O
@@ -327,6 +328,34 @@ def test_mapping_strict_rejects_and_nearest_maps():
     assert not cfg.exact and cfg.source == "nearest" and cfg.tile in legal_tiles("float32", False)
 
 
+def test_unmapped_schedule_fails_at_evaluation_by_default():
+    # no compile kwargs (as the reference's explorer calls it): the module
+    # compiles, its payload launches nothing and reports the mapping error,
+    # and the evaluator returns code 2 instead of timing another kernel
+    g = _matmul(4096, 4096, 4096)
+    b = Backend(g)
+    sch = b.get_scheduler()
+    for d, t in {"i": {"i1": 96}, "j": {"j1": 96}, "k": {"k1": 16}}.items():
+        sch.tile(d, t)
+    module = b.get_compiler().compile(sch.schedule())
+    assert "no float32 matmul kernel for block tile 96x96x16" in module.schedule_error
+    assert module.configs == {} and "xtc_hip_matmul(" not in module.source
+    res, code, msg = module.get_evaluator().evaluate()
+    assert (res, code) == ([], 2) and "no float32 matmul kernel" in msg
+    assert module.get_executor().execute() == 2
+    so = ctypes.CDLL(module.file_name)
+    getattr(so, module.payload_name)(None, None, None)
+    status = getattr(so, f"{module.payload_name}_status")
+    message = getattr(so, f"{module.payload_name}_message")
+    status.restype = ctypes.c_int
+    message.restype = ctypes.c_char_p
+    assert status() == 2 and b"no float32 matmul kernel" in message()
+    with pytest.raises(ScheduleError, match="no float32 matmul kernel"):
+        b.get_compiler(schedule_policy="strict").compile(sch.schedule())
+    nearest = b.get_compiler(schedule_policy="nearest").compile(sch.schedule())
+    assert nearest.schedule_error is None and not nearest.configs["C"].exact
+
+
 def test_mapping_split_k():
     attrs, s = _sched(_matmul(256, 256, 8192), {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 1024, "k2": 32}},
                       parallel=["k"])
@@ -470,3 +499,33 @@ def test_for_node_schedules_several_nodes():
     # a scheduler built on the shared states sees the same schedule
     other = b.get_scheduler(nodes_schedulers=sch.nodes_schedulers, default_node="fc1")
     assert other.schedule().node("fc2").tiles["j"] == {"j1": 128}
+
+
+# ---------------------------------------------------------------- bench workloads
+
+def test_bench_schedules_map_exactly():
+    from xtc_amd import configs
+
+    want = {
+        "C1": {"C": ((32, 32, 16, 1, 1), 4)},
+        "C2": {"C": ((256, 128, 32, 4, 2), 1)},
+        "C3a": {"C": ((256, 256, 32, 2, 4), 1)},
+        "C5": {"fc1": ((128, 256, 32, 2, 4), 1), "fc2": ((128, 128, 32, 2, 4), 2)},
+    }
+    for cfg, kernels in want.items():
+        b = Backend(configs.graph(cfg))
+        sch = configs.apply_schedule(b.get_scheduler(), cfg)
+        got = b.get_compiler(schedule_policy="strict").kernel_configs(sch.schedule())
+        assert {n: (c.tile, c.split_k) for n, c in got.items()} == kernels, cfg
+
+
+@pytest.mark.parametrize("cfg", ["C1", "C3b", "C4", "C5"])
+def test_bench_inputs_are_the_oracle_inputs(cfg):
+    from oracle import reference as ref
+    from xtc_amd import configs
+
+    got = configs.inputs(cfg, configs.graph(cfg))
+    want = ref.config_inputs(cfg)
+    assert len(got) == len(want)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)

@@ -126,6 +126,64 @@ def test_c3a_seeded_tuned_rows():
     assert ref.scaled_error(out[:, cols], expect, 8192, np.abs(a).max(), np.abs(b).max()) <= TOL_BF16
 
 
+# The schedules bench.py measures (xtc_amd.configs.SCHEDULES), each compiled
+# with the strict policy and checked on the seeded BASELINE inputs.
+BENCH_KERNELS = {
+    "C1": {"C": ((32, 32, 16, 1, 1), 4)},
+    "C2": {"C": ((256, 128, 32, 4, 2), 1)},
+    "C3a": {"C": ((256, 256, 32, 2, 4), 1)},
+    "C5": {"fc1": ((128, 256, 32, 2, 4), 1), "fc2": ((128, 128, 32, 2, 4), 2)},
+}
+
+
+def _bench_module(cfg):
+    from xtc_amd import configs
+
+    backend = Backend(configs.graph(cfg))
+    sch = configs.apply_schedule(backend.get_scheduler(), cfg)
+    module = backend.get_compiler(schedule_policy="strict").compile(sch.schedule())
+    got = {node: (c.tile, c.split_k) for node, c in module.configs.items()}
+    assert got == BENCH_KERNELS[cfg], got
+    return module
+
+
+def test_bench_schedule_c1_seeded():
+    a, b = ref.config_inputs("C1")
+    (out,) = _run(_bench_module("C1"), [a, b])
+    assert ref.scaled_error(out, ref.matmul(a, b), 512, 1.0, 1.0) <= TOL_F32
+
+
+def test_bench_schedule_c2_seeded():
+    a, b = ref.config_inputs("C2")
+    (out,) = _run(_bench_module("C2"), [a, b])
+    amax = (np.abs(a).max(), np.abs(b).max())
+    rows = slice(3, 4096, 9)
+    assert ref.scaled_error(out[rows], ref.matmul(a[rows], b), 4096, *amax) <= TOL_F32
+    cols = slice(4096 - 80, 4096)
+    expect = a.astype(np.float64) @ b[:, cols].astype(np.float64)
+    assert ref.scaled_error(out[:, cols], expect, 4096, *amax) <= TOL_F32
+
+
+def test_bench_schedule_c3a_seeded_rows_and_columns():
+    a, b = ref.config_inputs("C3a")
+    (out,) = _run(_bench_module("C3a"), [a, b])
+    amax = (np.abs(a).max(), np.abs(b).max())
+    # row bands across the first, a middle and the last tile rows
+    for rows in (slice(0, 64), slice(4000, 4160), slice(8192 - 96, 8192)):
+        assert ref.scaled_error(out[rows], ref.matmul(a[rows], b), 8192, *amax) <= TOL_BF16
+    # column bands through the whole M range: every tile row, two tile columns
+    for cols in (slice(0, 48), slice(8192 - 96, 8192)):
+        expect = a.astype(np.float64) @ b[:, cols].astype(np.float64)
+        assert ref.scaled_error(out[:, cols], expect, 8192, *amax) <= TOL_BF16
+
+
+def test_bench_schedule_c5_seeded():
+    x, w1, w2 = ref.config_inputs("C5")
+    (out,) = _run(_bench_module("C5"), [x, w1, w2])
+    h = ref.relu(ref.matmul(x, w1))
+    assert ref.scaled_error(out, ref.matmul(h, w2), 4096, np.abs(h).max(), np.abs(w2).max()) <= TOL_F32
+
+
 def test_c3b_seeded():
     a, b = ref.config_inputs("C3b")
     (out,) = _run(_compile(GRAPHS["C3b"]()), [a, b])

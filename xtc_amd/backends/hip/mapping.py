@@ -25,9 +25,11 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
 Tile semantics follow the reference: a tile size is the extent of the
 sub-loop (src/xtc/backends/mlir/MlirCompilerPasses.py:414-457).
 
-A request that matches no compiled instance is either rejected
-(policy "strict") or mapped to the nearest instance in log2 distance
-(policy "nearest", the default); the result records which happened.
+A request that matches no compiled instance is either rejected with
+ScheduleError (policy "strict", the default) or mapped to the nearest
+instance in log2 distance (policy "nearest", opt-in); the result records
+which happened.  The compiler's default policy "report" maps with "strict"
+and turns the error into a module that fails when evaluated (compiler.py).
 """
 
 from __future__ import annotations
@@ -126,7 +128,7 @@ def map_gemm(
     launch_attrs: dict[str, Any],
     conv: bool,
     sched: HipNodeSchedule | None,
-    policy: str = "nearest",
+    policy: str = "strict",
 ) -> GemmConfig:
     dtype = launch_attrs["dtype"]
     M, N, K = launch_attrs["M"], launch_attrs["N"], launch_attrs["K"]

@@ -4,7 +4,10 @@
 #include <hip/hip_runtime.h>
 
 #include <dlfcn.h>
+#include <linux/perf_event.h>
 #include <math.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -1299,6 +1302,56 @@ bool pmu_hooks(PmuHooks* h) {
   return h->ready && h->open && h->start && h->stop && h->close && h->ready();
 }
 
+constexpr int kMaxEvents = 64;
+thread_local int g_eval_status = 0;
+
+// Host counters of the reference's perf_event backend, by the names of
+// perf_event_linux.c:37-54 (generic hardware and software events of
+// perf_event_open; names that need libpfm are not known here).
+struct HostEventDecl {
+  const char* name;
+  uint32_t type;
+  uint64_t config;
+};
+const HostEventDecl kHostEvents[] = {
+    {"cycles", PERF_TYPE_HARDWARE, PERF_COUNT_HW_CPU_CYCLES},
+    {"clocks", PERF_TYPE_SOFTWARE, PERF_COUNT_SW_CPU_CLOCK},
+    {"instructions", PERF_TYPE_HARDWARE, PERF_COUNT_HW_INSTRUCTIONS},
+    {"migrations", PERF_TYPE_SOFTWARE, PERF_COUNT_SW_CPU_MIGRATIONS},
+    {"context_switches", PERF_TYPE_SOFTWARE, PERF_COUNT_SW_CONTEXT_SWITCHES},
+    {"cache_access", PERF_TYPE_HARDWARE, PERF_COUNT_HW_CACHE_REFERENCES},
+    {"cache_misses", PERF_TYPE_HARDWARE, PERF_COUNT_HW_CACHE_MISSES},
+    {"branches", PERF_TYPE_HARDWARE, PERF_COUNT_HW_BRANCH_INSTRUCTIONS},
+    {"branches_misses", PERF_TYPE_HARDWARE, PERF_COUNT_HW_BRANCH_MISSES},
+};
+
+// A counting perf event for `name` on the calling process, user space only,
+// inherited by threads it creates later (the attributes of
+// perf_event_linux.c:72-81); -1 if the name is unknown or the kernel refuses
+// it (no hardware PMU, perf_event_paranoid).
+int open_host_event(const char* name) {
+  for (const HostEventDecl& d : kHostEvents) {
+    if (strcmp(name, d.name)) continue;
+    struct perf_event_attr attr;
+    memset(&attr, 0, sizeof(attr));
+    attr.size = sizeof(attr);
+    attr.type = d.type;
+    attr.config = d.config;
+    attr.exclude_kernel = 1;
+    attr.exclude_hv = 1;
+    attr.exclude_idle = 1;
+    attr.inherit = 1;
+    return (int)syscall(SYS_perf_event_open, &attr, 0, -1, -1, 0);
+  }
+  return -1;
+}
+
+uint64_t read_host_event(int fd) {
+  uint64_t v = 0;
+  if (read(fd, &v, sizeof(v)) != (ssize_t)sizeof(v)) return 0;
+  return v;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1306,34 +1359,51 @@ extern "C" {
 void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_names[],
                            int repeat, int number, int min_repeat_ms, void (*func)(void),
                            void** args, int nargs) {
-  if (!results || repeat <= 0 || number < 0 || min_repeat_ms < 0 || !func || nargs < 0 ||
-      nargs > 8) {
+  g_eval_status = 0;
+  g_last_error.clear();
+  if (!results || repeat <= 0 || number < 0 || min_repeat_ms < 0 || !func || nargs < 0 || nargs > 8 ||
+      events_num < 0 || (events_num > 0 && !events_names)) {
+    g_eval_status = 1;
     fail("evaluate_perf: invalid arguments");
+    return;
+  }
+  if (events_num > kMaxEvents) {
+    g_eval_status = 1;
+    fail("evaluate_perf: %d events requested, at most %d", events_num, kMaxEvents);
     return;
   }
   // event kinds: 0 unknown, 1 gpu.time (s), 2 gpu.clocks (ns), 3 hardware
   // counter gpu.<name> (gpu.cycles = GRBM_GUI_ACTIVE, the GPU's busy cycles)
-  // read through libxtc_hip_pmu when the process loaded and enabled it
-  int kinds[16] = {0};
-  if (events_num > 16) events_num = 16;
-  const char* pmu_names[16];
-  int pmu_of_event[16];
-  int pmu_slot[16];
+  // read through libxtc_hip_pmu when the process loaded and enabled it, 4 a
+  // host counter of perf_event_open (perf_event_linux.c:37-54 names)
+  int kinds[kMaxEvents] = {0};
+  const char* pmu_names[kMaxEvents];
+  int pmu_of_event[kMaxEvents];
+  int pmu_slot[kMaxEvents];
+  int host_fd[kMaxEvents];
+  uint64_t host_start[kMaxEvents] = {0};
+  double host_delta[kMaxEvents] = {0};
   int npmu = 0;
   for (int e = 0; e < events_num; ++e) {
     const char* n = events_names[e];
+    host_fd[e] = -1;
     kinds[e] = (n && !strcmp(n, "gpu.time")) ? 1 : (n && !strcmp(n, "gpu.clocks")) ? 2 : 0;
     if (kinds[e] == 0 && n && !strncmp(n, "gpu.", 4)) {
       kinds[e] = 3;
       pmu_of_event[e] = npmu;
       pmu_names[npmu++] = !strcmp(n + 4, "cycles") ? "GRBM_GUI_ACTIVE" : n + 4;
+    } else if (kinds[e] == 0 && n) {
+      host_fd[e] = open_host_event(n);
+      if (host_fd[e] >= 0) kinds[e] = 4;
     }
   }
   PmuHooks pmu;
   const bool pmu_on = npmu > 0 && pmu_hooks(&pmu) && pmu.open(g_current, npmu, pmu_names, pmu_slot) == 0;
-  double pmu_sums[16] = {0};
+  double pmu_sums[kMaxEvents] = {0};
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  const bool use_events = events_num > 0 && current_state();
+  bool use_events = false;
+  for (int e = 0; e < events_num; ++e) use_events = use_events || kinds[e] == 1 || kinds[e] == 2;
+  use_events = use_events && current_state();
   if (use_events) {
     hipEventCreate(&ev0);
     hipEventCreate(&ev1);
@@ -1351,9 +1421,13 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
     while (1) {
       if (pmu_on) pmu_ok = pmu.start() == 0;
       if (use_events) hipEventRecord(ev0, current_state()->stream);
+      for (int e = 0; e < events_num; ++e)
+        if (kinds[e] == 4) host_start[e] = read_host_event(host_fd[e]);
       double t0 = now_s();
       for (int a = 0; a < attempts; ++a) call_payload(func, args, nargs);
       elapsed = now_s() - t0;
+      for (int e = 0; e < events_num; ++e)
+        if (kinds[e] == 4) host_delta[e] = (double)(read_host_event(host_fd[e]) - host_start[e]);
       if (use_events) {
         hipEventRecord(ev1, current_state()->stream);
         hipEventSynchronize(ev1);
@@ -1361,7 +1435,7 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
       }
       if (pmu_on) {
         hipDeviceSynchronize();  // every dispatch of the window has completed
-        pmu_ok = pmu.stop(pmu_sums, 16) == 0 && pmu_ok;
+        pmu_ok = pmu.stop(pmu_sums, kMaxEvents) == 0 && pmu_ok;
       }
       if (elapsed * 1000.0 >= (double)min_repeat_ms) break;
       attempts *= 2;
@@ -1373,18 +1447,23 @@ void xtc_hip_evaluate_perf(double* results, int events_num, const char* events_n
         if (use_events && kinds[e] == 2) v = (double)dev_ms * 1e6 / attempts;
         if (kinds[e] == 3 && pmu_ok && pmu_slot[pmu_of_event[e]] >= 0)
           v = pmu_sums[pmu_slot[pmu_of_event[e]]] / attempts;
+        if (kinds[e] == 4) v = host_delta[e] / attempts;
         results[r * events_num + e] = v;
       }
     } else {
       results[r] = elapsed / attempts;
     }
   }
+  for (int e = 0; e < events_num; ++e)
+    if (host_fd[e] >= 0) close(host_fd[e]);
   if (pmu_on) pmu.close();
   if (use_events) {
     hipEventDestroy(ev0);
     hipEventDestroy(ev1);
   }
 }
+
+int xtc_hip_evaluate_status(void) { return g_eval_status; }
 
 void xtc_hip_evaluate(double* results, int repeat, int number, int min_repeat_ms,
                       void (*func)(void), void** args, int nargs) {

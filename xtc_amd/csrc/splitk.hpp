@@ -23,7 +23,8 @@
 // whole L2 of the XCD in every workgroup, which costs more than the reduce.
 // The 16-byte accesses halve the instructions of the 8-byte atomic pairs
 // they replaced and make the C5 MLP 4 % faster.
-// Counters start at zero (the host clears them once when it allocates them)
+// Counters start at zero (the host clears them with a kernel when it
+// allocates them, and before every call of the no-allocation entry point)
 // and every launch leaves them at zero.  Two launches that share the
 // counters and the workspace must not overlap: the host keeps both per
 // launch stream.
@@ -50,10 +51,14 @@ __device__ __forceinline__ float splitk_load(const float* p) {
 // 16-byte aligned p: one 16-byte store with the agent-scope cache policy
 // (sc1, what an agent-scope atomic store of 8 bytes compiles to), issued from
 // asm because no atomic is 16 bytes wide; its completion is waited for in
-// splitk_arrive (s_waitcnt vmcnt(0)).  The s_nop covers the one wait state a
-// VALU write of the data registers needs after a store of more than 8 bytes.
+// splitk_arrive (s_waitcnt vmcnt(0)).  The compiler does not count wait
+// states into inline asm, so the asm opens with 24 of them: the most an
+// MFMA result needs before a memory instruction reads it (16-pass XDL ops
+// need 19).  The trailing s_nop covers the one wait state a VALU write of
+// the data registers needs after a store of more than 8 bytes.
 __device__ __forceinline__ void splitk_store4(float* p, splitk::f32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\tglobal_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" ::"v"(p), "v"(v)
+               : "memory");
 }
 
 __device__ __forceinline__ splitk::f32x4 splitk_load4(const float* p) {

@@ -181,6 +181,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         None,
         [ctypes.POINTER(ctypes.c_double), _i, _i, _i, _vp, ctypes.POINTER(_vp), _i],
     ),
+    "xtc_hip_evaluate_status": (_i, []),
     "xtc_hip_evaluate_flops": (ctypes.c_double, [ctypes.c_char_p]),
 }
 

@@ -154,8 +154,11 @@ class HipDevice(AcceleratorDevice):
         """Times `cfunc(*args)` with the evaluate_perf protocol.
 
         Without events: seconds per call (wall clock around synchronous
-        calls).  Events: "gpu.time" (device seconds per call, HIP events),
-        "gpu.clocks" (device ns per call); unknown names give -1.
+        calls).  Events, per call: "gpu.time" (device seconds, HIP events),
+        "gpu.clocks" (device ns), "gpu.<counter>" (GPU hardware counters,
+        xtc_amd.runtimes.hip.pmu), and the host counters "cycles", "clocks",
+        "instructions", ... of perf_event_open; names that cannot be opened
+        give -1.
         """
         self.init_device()
         nvals = max(1, len(pmu_events))
@@ -163,10 +166,10 @@ class HipDevice(AcceleratorDevice):
         names = (ctypes.c_char_p * max(1, len(pmu_events)))(*[e.encode() for e in pmu_events])
         fptr = ctypes.cast(cfunc, ctypes.c_void_p)
         argv = (ctypes.c_void_p * max(1, nargs))(*[ctypes.cast(a, ctypes.c_void_p).value if not isinstance(a, int) else a for a in list(args)[:nargs]])
-        capi.lib().xtc_hip_evaluate_perf(results, len(pmu_events), names, repeat, number, min_repeat_ms, fptr, argv, nargs)
-        err = capi.last_error()
-        if err.startswith("evaluate_perf"):
-            raise capi.HipError(err)
+        L = capi.lib()
+        L.xtc_hip_evaluate_perf(results, len(pmu_events), names, repeat, number, min_repeat_ms, fptr, argv, nargs)
+        if L.xtc_hip_evaluate_status():
+            raise capi.HipError(capi.last_error())
         return [float(v) for v in results]
 
     def evaluate(self, results: Any, repeat: int, number: int, nargs: int, cfunc: Any, args: Any) -> None:

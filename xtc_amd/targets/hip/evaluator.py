@@ -98,6 +98,8 @@ class HipEvaluator(Evaluator):
         return rc, (msg() or b"").decode()
 
     def evaluate(self) -> tuple[list[float], int, str]:
+        if getattr(self._module, "schedule_error", None):
+            return ([], 2, f"Error in compilation: schedule: {self._module.schedule_error}")
         dev = self._device
         hw = [c for c in self._pmu_counters if pmu.is_hardware_counter(c)]
         if hw and not pmu.registered():

@@ -74,6 +74,7 @@ class HipModule(Module):
         source: str = "",
         device: int = 0,
         bare_ptr: bool = True,
+        schedule_error: str | None = None,
     ) -> None:
         self._name = name
         self._payload_name = payload_name
@@ -84,6 +85,9 @@ class HipModule(Module):
         self.source = source
         self.device = device
         self._bare_ptr = bare_ptr
+        # set when the schedule mapped onto no kernel (compile policy
+        # "report"): the payload launches nothing and reports this message
+        self.schedule_error = schedule_error
         self._np_inputs_spec = graph_np_inputs_spec(graph)
         self._np_outputs_spec = graph_np_outputs_spec(graph)
         self._reference_impl = graph_reference_impl(graph)
