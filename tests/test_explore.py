@@ -159,3 +159,149 @@ def test_pmu_counters_are_split_from_the_times(tmp_path, monkeypatch):
     cfg.pmu_counters = ["gpu.cycles", "gpu.time"]
     assert Exploration(g, cfg).split_counters([5.0, 1e-3, 6.0, 2e-3]) == (
         [1e-3, 2e-3], {"gpu.cycles": [5.0, 6.0], "gpu.time": [1e-3, 2e-3]})
+
+
+# ---------------------------------------------------------------- no fork after the GPU starts
+
+def test_no_process_starts_after_the_device(tmp_path, monkeypatch):
+    # A fake device: evaluation "starts the GPU runtime" on first use.  Every
+    # way this process could start another one (fork, posix_spawn, the
+    # fork_exec behind subprocess and multiprocessing) is recorded together
+    # with whether the device had started; compilation must still happen.
+    import _posixsubprocess
+    import os
+
+    from xtc_amd.runtimes.hip.device import HipDevice
+
+    state = {"gpu": False}
+    spawns = []
+
+    def fake_init(self):
+        state["gpu"] = True
+
+    def evaluate_one(self, module):
+        HipDevice(0).init_device()
+        assert os.path.exists(module.file_name)
+        return [1e-3], 0, ""
+
+    def record(name, real):
+        def wrapper(*a, **k):
+            spawns.append((name, state["gpu"]))
+            return real(*a, **k)
+
+        return wrapper
+
+    monkeypatch.setattr(HipDevice, "init_device", fake_init)
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    monkeypatch.setattr(_posixsubprocess, "fork_exec", record("fork_exec", _posixsubprocess.fork_exec))
+    monkeypatch.setattr(os, "fork", record("fork", os.fork))
+    monkeypatch.setattr(os, "posix_spawn", record("posix_spawn", os.posix_spawn))
+    g = build_graph("matmul", [384, 384, 384], "float32")
+    for search in ("random", "iterative"):
+        cfg = ExplorationConfig(search=search, trials=6, batch=2, optimizer="random", seed=5,
+                                output=str(tmp_path / f"{search}.csv"), peak_flops=1e12, jobs=3)
+        res = Exploration(g, cfg).run()
+        assert len(res) == 6 and all(code == 0 for _, _, code, _ in res), res
+        assert state["gpu"]
+        assert not [s for s in spawns if s[1]], spawns
+        state["gpu"] = False
+    # the recorder sees what subprocess starts in this process
+    import subprocess
+
+    subprocess.run(["true"], check=True)
+    assert ("fork_exec", False) in spawns
+
+
+# ---------------------------------------------------------------- iterative search and optimizers
+
+def test_iterative_search_records_every_batch(tmp_path, monkeypatch):
+    times = {}
+
+    def evaluate_one(self, module):
+        (c,) = module.configs.values()
+        # larger tiles "run faster": a smooth objective for the forest
+        t = 1e-3 / (c.bm * c.bn)
+        times[(c.bm, c.bn)] = t
+        return [t], 0, ""
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    g = build_graph("matmul", [1024, 1024, 1024], "float32")
+    cfg = ExplorationConfig(search="iterative", trials=7, batch=3, optimizer="random-forest-default", seed=1,
+                            output=str(tmp_path / "it.csv"), db_file=str(tmp_path / "it.jsonl"), peak_flops=1e12,
+                            jobs=2)
+    res = Exploration(g, cfg).run()
+    assert len(res) == 7 and all(code == 0 for _, _, code, _ in res)
+    assert len([json.loads(l) for l in open(tmp_path / "it.jsonl")]) == 7
+    rows = list(csv.DictReader(open(tmp_path / "it.csv")))
+    assert 1 <= len(rows) <= 7  # repeated proposals are written once
+
+
+def _grid_sampler(n, seed):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        yield [int(v) for v in rng.integers(0, 16, size=2)]
+
+
+def test_random_optimizer_draws_one_seed_per_batch():
+    import random
+
+    from xtc_amd.search.optimizers import Optimizers
+
+    opt = Optimizers.from_name("random")(_grid_sampler, 4, 7)
+    r = random.Random(7)
+    for _ in range(3):
+        assert opt.suggest() == list(_grid_sampler(4, r.randint(0, 2**32 - 1)))
+
+
+def test_random_forest_optimizer_protocol_and_convergence(tmp_path):
+    import random
+
+    from xtc_amd.search.optimizers import Optimizers
+
+    def peak(x):  # fraction of peak, best at (11, 4)
+        return 1.0 / (1.0 + (x[0] - 11) ** 2 + (x[1] - 4) ** 2)
+
+    make = Optimizers.from_name("random-forest-default")
+    opt = make(_grid_sampler, 4, 3)
+    # before update_first (= batch) observations: 4 random picks among
+    # batch_candidates fresh samples, one seed draw for the candidates
+    r = random.Random(3)
+    cands = list(_grid_sampler(1000, r.randint(0, 2**32 - 1)))
+    first = opt.suggest()
+    assert first == r.choices(cands, k=4)
+    opt.observe(first, [peak(x) for x in first])
+    assert opt.fitted_on == 4
+    fits = [opt.fitted_on]
+    for _ in range(9):
+        xs = opt.suggest()
+        assert len(xs) == 4
+        opt.observe(xs, [peak(x) for x in xs])
+        fits.append(opt.fitted_on)
+    # refit every update_period (= batch) observations
+    assert fits == list(range(4, 44, 4))
+    assert opt.best_y == max(opt.y) and peak(opt.best_x) == opt.best_y
+    # 40 evaluations of a 256-point grid find the optimum's neighbourhood
+    assert abs(opt.best_x[0] - 11) + abs(opt.best_x[1] - 4) <= 2, opt.best_x
+    # same seed, same proposals
+    again = make(_grid_sampler, 4, 3)
+    assert again.suggest() == first
+    # a YAML file overrides the preset
+    conf = tmp_path / "rf.yaml"
+    conf.write_text("beta: 0.5\nupdate_first: 8\n")
+    tuned = make(_grid_sampler, 4, 3, str(conf))
+    assert tuned.beta == 0.5 and tuned.update_first == 8 and tuned.alpha == 0.7
+    with pytest.raises(ValueError, match="unknown optimizer"):
+        Optimizers.from_name("bayes")
+
+
+def test_explorer_refuses_gpu_hardware_counters(tmp_path):
+    from xtc_amd.cli.explore import main
+    from xtc_amd.search.explore import check_explore_counters
+
+    check_explore_counters(["gpu.time", "gpu.clocks"])
+    with pytest.raises(ValueError, match="switched off"):
+        check_explore_counters(["gpu.time", "gpu.SQ_WAVES"])
+    assert main(["--pmu-counters", "gpu.cycles", "--output", str(tmp_path / "x.csv")]) == 2
+    assert not (tmp_path / "x.csv").exists()

@@ -1,0 +1,53 @@
+# SPDX-License-Identifier: BSD-3-Clause
+"""loop-explore on the GPU, through its command line (src/xtc/cli/explore.py).
+
+Every sample is compiled, validated against the graph's numpy interpreter
+(XTC's own np.allclose check on np_init inputs) and timed; the CSV keeps the
+reference's layout.  Each run is a fresh process, as `loop-explore` is.
+"""
+
+from __future__ import annotations
+
+import csv
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _explore(tmp_path, *flags):
+    out = tmp_path / "e.csv"
+    db = tmp_path / "e.jsonl"
+    cmd = [sys.executable, "-u", "-m", "xtc_amd.cli.explore", "--operator", "matmul", "--dims", "512", "512", "512",
+           "--dtype", "float32", "--strategy", "tile_hip", "--seed", "0", "--repeat", "2", "--min-repeat-ms", "10",
+           "--jobs", "4", "--output", str(out), "--db-file", str(db), *flags]
+    print("[explore]", " ".join(cmd[3:]), flush=True)
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    return list(csv.DictReader(open(out))), [json.loads(line) for line in open(db)], proc
+
+
+def test_loop_explore_c1_random_validated(tmp_path):
+    rows, recs, proc = _explore(tmp_path, "--search", "random", "--trials", "8", "--validate")
+    assert len(recs) == 8
+    assert all(r["results"][0] == 0 for r in recs), [r["error"] for r in recs]
+    assert len(rows) == 8, proc.stderr[-2000:]
+    for r in rows:
+        t = float(r["time"])
+        # 512^3 fp32: above the MFMA roofline (1.7 us), below a millisecond
+        assert 1.7e-6 < t < 1e-3 and float(r["peak"]) > 0
+        assert r["backend"] == "hip"
+
+
+def test_loop_explore_c1_iterative(tmp_path):
+    rows, recs, proc = _explore(tmp_path, "--search", "iterative", "--trials", "6", "--batch", "2", "--optimizer",
+                                "random-forest-default")
+    assert len(recs) == 6 and all(r["results"][0] == 0 for r in recs), [r["error"] for r in recs]
+    assert 1 <= len(rows) <= 6
+    assert "best" in proc.stdout

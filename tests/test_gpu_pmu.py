@@ -100,8 +100,9 @@ def test_gpu_counters_need_enable_before_the_runtime():
     assert out["code2"] == 0 and len(out["res2"]) == 1 and out["res2"][0] > 0
 
 
-@pytest.mark.skip(reason="stalled once with no output for over 180 s on a GPU box (the run was stopped); the cause "
-                         "is not shown: kept off the GPU until it is")
+@pytest.mark.skip(reason="loop-explore with GPU hardware counters stalled until killed on MI355X twice (the second "
+                         "run with the payload compiler out of process); the cause is not found, so the explorer "
+                         "refuses hardware counters and this case stays off the GPU")
 def test_explore_records_counters_per_sample(tmp_path):
     # loop-explore with --pmu-counters in a fresh process (XTC_HIP_PMU=1
     # registers the counter tool when the library loads, before any GPU
@@ -117,7 +118,7 @@ def test_explore_records_counters_per_sample(tmp_path):
            "--repeat", "2", "--min-repeat-ms", "0", "--jobs", "2", "--output", str(out), "--db-file", str(db),
            "--pmu-counters", "gpu.SQ_WAVES"]
     print("[explore pmu]", " ".join(cmd[3:]), flush=True)
-    proc = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True, timeout=240)
+    proc = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stderr[-3000:]
     rows = list(csv.DictReader(open(out)))
     recs = [json.loads(l) for l in open(db)]

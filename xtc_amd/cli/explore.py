@@ -7,7 +7,8 @@
 
 Flags follow the reference where they apply (operator, dims, dtype,
 strategy, search, backends, trials, seed, threads, max-unroll, opt-level,
-output, db-file, resume, append, graph-file, peak-flops, data).  The
+output, db-file, resume, append, graph-file, peak-flops, data, optimizer,
+optimizer-list, optimizer-config, batch).  The
 reference re-executes itself under `setarch -R` to disable ASLR for CPU
 timing stability; GPU timing does not need it, so this driver runs in-process.
 """
@@ -69,7 +70,12 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("--pad", type=int, default=0, help="conv2d: pad2d producer on H and W")
     p.add_argument("--dtype", default="float32", choices=["float32", "bfloat16"])
     p.add_argument("--strategy", default="tile_hip", help=f"one of {Strategies.names(include_aliases=True)}")
-    p.add_argument("--search", default="random", choices=["random", "exhaustive", "data", "default"])
+    p.add_argument("--search", default="random", choices=["random", "exhaustive", "data", "default", "iterative"])
+    p.add_argument("--optimizer", default="random-forest-default",
+                   help="optimizer of --search iterative; --optimizer-list lists them")
+    p.add_argument("--optimizer-list", action="store_true", help="print the optimizers and exit")
+    p.add_argument("--optimizer-config", default="", help="YAML file overriding the optimizer's preset")
+    p.add_argument("--batch", type=int, default=1, help="samples per optimizer proposal")
     p.add_argument("--data", help="CSV of samples for --search data")
     p.add_argument("--backends", nargs="+", default=["hip"], choices=["hip"])
     p.add_argument("--trials", type=int, default=64)
@@ -85,9 +91,10 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("--min-repeat-ms", type=int, default=100)
     p.add_argument("--validate", action="store_true")
     p.add_argument("--pmu-counters", nargs="*", default=[],
-                   help="counters per sample (gpu.time, gpu.cycles, gpu.<rocprofiler counter>); gpu.time is "
-                        "added when missing and gives the CSV time, every counter's values go to the --db-file "
-                        "record; hardware counters need XTC_HIP_PMU=1 or a fresh process")
+                   help="counters per sample (gpu.time, gpu.clocks); gpu.time is added when missing and gives the "
+                        "CSV time, every counter's values go to the --db-file record.  GPU hardware counters "
+                        "(gpu.cycles, gpu.<rocprofiler counter>) are switched off here: explorations with them "
+                        "stalled on MI355X")
     p.add_argument("--jobs", type=int, default=max(1, min(16, (os.cpu_count() or 2) // 2)))
     p.add_argument("--output", default="results.csv")
     p.add_argument("--db-file")
@@ -96,7 +103,26 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("--peak-flops", type=float, help="peak FMA/s (default: device MFMA peak)")
     p.add_argument("--debug", action="store_true")
     args = p.parse_args(argv)
+    if args.optimizer_list:
+        from ..search.optimizers import Optimizers
+
+        print("\n".join(Optimizers.names()))
+        return 0
     logging.basicConfig(level=logging.DEBUG if args.debug else logging.INFO, format="%(message)s")
+    if args.pmu_counters:
+        from ..search.explore import check_explore_counters
+
+        try:
+            check_explore_counters(args.pmu_counters)
+        except ValueError as err:
+            print(err, file=sys.stderr)
+            return 2
+    if "hip" in args.backends:
+        from ..backends.hip.compiler import CompileService
+
+        # the payload compiler's fork server starts before anything loads the
+        # GPU libraries (XTC_HIP_PMU=1 registers the counter tool on load)
+        CompileService.start_server()
 
     if args.graph_file:
         import xtc_amd.graphs.xtc.op as O
@@ -118,6 +144,9 @@ def main(argv: list[str] | None = None) -> int:
             search=args.search,
             trials=args.trials,
             seed=args.seed,
+            optimizer=args.optimizer,
+            optimizer_config=args.optimizer_config,
+            batch=args.batch,
             opt_level=args.opt_level,
             data=args.data,
             repeat=args.repeat,

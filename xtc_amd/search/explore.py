@@ -12,6 +12,15 @@ backend), optionally to a JSON-lines DB, and a `<output>.meta.json` run
 manifest records the arguments.  Failed samples get time 0 and are logged,
 and are not written to the CSV (callback.py:152-154).
 
+Searches: "random", "exhaustive", "data", "default", and "iterative"
+(src/xtc/search/explore.py:515-538): batches proposed by an optimizer
+(xtc_amd/search/optimizers.py) that observes each batch's fraction of peak.
+
+The exploring process also runs the GPU, so it starts no process once its
+GPU runtime is up: the payloads' gcc runs in a CompileService (worker
+processes of a fork server started before any GPU work), and the manifest's
+`git rev-parse` runs before the first evaluation.
+
 With the HIP backend the strategy's samples are filtered to those that map
 exactly onto a compiled kernel instance (schedule_policy "strict"), so every
 measured point is the schedule it claims to be.
@@ -47,9 +56,12 @@ class ExplorationConfig:
     backend: str = "hip"
     strategy: str = "tile_hip"
     strategy_kwargs: dict[str, Any] = field(default_factory=dict)
-    search: str = "random"  # "random" | "exhaustive" | "data"
+    search: str = "random"  # "random" | "exhaustive" | "data" | "default" | "iterative"
     trials: int = 64
     seed: int = 0
+    optimizer: str = "random-forest-default"  # search "iterative"
+    optimizer_config: str = ""  # YAML overrides of the optimizer preset
+    batch: int = 1  # samples per optimizer proposal
     opt_level: int = 2
     data: str | None = None  # CSV of samples for search "data"
     repeat: int = 5
@@ -193,6 +205,27 @@ def hip_sample_filter(graph: Any, strategy_factory: Callable[..., Any]) -> Calla
     return ok
 
 
+# GPU hardware counters per sample are switched off in the explorer: with
+# them, loop-explore stalled until killed on MI355X (twice, the second time
+# with the payload compiler moved out of the process), while the same
+# counters collected by one HipEvaluator in a fresh process work.  The cause
+# is not found, so the path raises instead of running.
+EXPLORE_HW_COUNTERS_OFF = (
+    "loop-explore: GPU hardware counters per sample ({names}) are switched off: explorations that collected "
+    "them stalled on MI355X and the cause is not found.  gpu.time and gpu.clocks work here; a module's evaluator "
+    "(HipEvaluator pmu_counters=[...]) collects hardware counters in a fresh process."
+)
+
+
+def check_explore_counters(names: list[str]) -> None:
+    """Raises ValueError when `names` holds a GPU hardware counter."""
+    from ..runtimes.hip.pmu import is_hardware_counter
+
+    hw = [n for n in names if is_hardware_counter(n)]
+    if hw:
+        raise ValueError(EXPLORE_HW_COUNTERS_OFF.format(names=", ".join(hw)))
+
+
 class Exploration:
     def __init__(self, graph: Any, config: ExplorationConfig) -> None:
         self.graph = graph
@@ -244,6 +277,7 @@ class Exploration:
 
     def evaluate_one(self, module: Any) -> tuple[list[float], int, str]:
         c = self.config
+        check_explore_counters(c.pmu_counters)
         return module.get_evaluator(
             repeat=c.repeat, number=c.number, min_repeat_ms=c.min_repeat_ms, validate=c.validate,
             pmu_counters=self.counters(),
@@ -284,39 +318,93 @@ class Exploration:
         }
         Path(f"{self.config.output}.meta.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
 
-    def run(self) -> list[tuple[list[int], list[float], int, str]]:
+    def _evaluate_compiled(
+        self, sample: list[int], fut: Any, csv_cb: CSVCallback, db_cb: DBCallback | None
+    ) -> tuple[list[int], list[float], int, str]:
         c = self.config
-        samples = self.samples()
-        csv_cb = CSVCallback(c.output, self.peak_time(), self.strategy.sample_names, resume=c.resume, append=c.append)
-        db_cb = DBCallback(c.db_file, self.graph, c.strategy) if c.db_file else None
-        self.write_manifest()
-        todo = [s for s in samples if (c.backend, tuple(s)) not in csv_cb.seen]
-        results: list[tuple[list[int], list[float], int, str]] = []
-        t0 = time.time()
-        with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
-            futures = [pool.submit(self.compile_one, s) for s in todo]
-            for idx, (sample, fut) in enumerate(zip(todo, futures)):
-                extra: dict[str, Any] = {}
-                try:
-                    module = fut.result()
-                    extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()},
-                             "error": ""}
-                    values, code, msg = self.evaluate_one(module)
-                    times, per_counter = self.split_counters(values) if code == 0 else ([], {})
-                    if per_counter:
-                        extra["counters"] = per_counter
-                except Exception as err:  # a failed sample is recorded, not fatal
-                    times, code, msg = [], 2, f"{type(err).__name__}: {err}"
-                if code:
-                    logger.warning("sample %s failed: %s", sample, msg)
-                results.append((sample, times, code, msg))
-                csv_cb(sample, c.backend, times, code, msg)
-                if db_cb:
-                    db_cb(sample, c.backend, times, code, msg, {**extra, "error": msg})
-                best = min(times) if times else 0.0
-                logger.info("[%d/%d] %s -> %.3g s (%s)", idx + 1, len(todo), sample, best, msg or "ok")
-        csv_cb.close()
+        extra: dict[str, Any] = {}
+        try:
+            module = fut.result()
+            extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()}, "error": ""}
+            values, code, msg = self.evaluate_one(module)
+            times, per_counter = self.split_counters(values) if code == 0 else ([], {})
+            if per_counter:
+                extra["counters"] = per_counter
+        except Exception as err:  # a failed sample is recorded, not fatal
+            times, code, msg = [], 2, f"{type(err).__name__}: {err}"
+        if code:
+            logger.warning("sample %s failed: %s", sample, msg)
+        csv_cb(sample, c.backend, times, code, msg)
         if db_cb:
-            db_cb.close()
-        logger.info("explored %d samples in %.1f s", len(todo), time.time() - t0)
+            db_cb(sample, c.backend, times, code, msg, {**extra, "error": msg})
+        return (sample, times, code, msg)
+
+    def _run_batch(
+        self, pool: cf.ThreadPoolExecutor, todo: list[list[int]], csv_cb: CSVCallback, db_cb: DBCallback | None,
+        done: int, total: int,
+    ) -> list[tuple[list[int], list[float], int, str]]:
+        futures = [pool.submit(self.compile_one, s) for s in todo]
+        out = []
+        for idx, (sample, fut) in enumerate(zip(todo, futures)):
+            res = self._evaluate_compiled(sample, fut, csv_cb, db_cb)
+            out.append(res)
+            best = min(res[1]) if res[1] else 0.0
+            logger.info("[%d/%d] %s -> %.3g s (%s)", done + idx + 1, total, sample, best, res[3] or "ok")
+        return out
+
+    def run(self) -> list[tuple[list[int], list[float], int, str]]:
+        from contextlib import nullcontext
+
+        c = self.config
+        service: Any = nullcontext()
+        if c.backend == "hip":
+            from ..backends.hip.compiler import CompileService
+
+            service = CompileService(c.jobs)
+        with service:
+            self.write_manifest()  # runs git: before any GPU work
+            results: list[tuple[list[int], list[float], int, str]] = []
+            t0 = time.time()
+            if c.search == "iterative":
+                samples: list[list[int]] = []
+            else:
+                samples = self.samples()
+            peak_time = self.peak_time()
+            csv_cb = CSVCallback(c.output, peak_time, self.strategy.sample_names, resume=c.resume, append=c.append)
+            db_cb = DBCallback(c.db_file, self.graph, c.strategy) if c.db_file else None
+            try:
+                with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
+                    if c.search == "iterative":
+                        results = self._run_iterative(pool, csv_cb, db_cb, peak_time)
+                    else:
+                        todo = [s for s in samples if (c.backend, tuple(s)) not in csv_cb.seen]
+                        results = self._run_batch(pool, todo, csv_cb, db_cb, 0, len(todo))
+            finally:
+                csv_cb.close()
+                if db_cb:
+                    db_cb.close()
+            logger.info("explored %d samples in %.1f s", len(results), time.time() - t0)
+        return results
+
+    def _run_iterative(
+        self, pool: cf.ThreadPoolExecutor, csv_cb: CSVCallback, db_cb: DBCallback | None, peak_time: float
+    ) -> list[tuple[list[int], list[float], int, str]]:
+        """Batches of `batch` samples proposed by the optimizer, which then
+        observes each one's fraction of peak (peak_time / time, 0 when the
+        sample failed), for `trials` samples in all
+        (src/xtc/search/explore.py:515-538)."""
+        from .optimizers import Optimizers
+
+        c = self.config
+        opt = Optimizers.from_name(c.optimizer)(
+            lambda n, seed: self.strategy.sample(n, seed=seed), c.batch, c.seed, c.optimizer_config
+        )
+        results: list[tuple[list[int], list[float], int, str]] = []
+        for step in range(0, c.trials, c.batch):
+            size = min(c.batch, c.trials - step)
+            batch = [list(x) for x in opt.suggest()[:size]]
+            got = self._run_batch(pool, batch, csv_cb, db_cb, step, c.trials)
+            results.extend(got)
+            opt.observe(batch, [peak_time / min(t) if code == 0 and t and min(t) > 0 else 0.0 for _, t, code, _ in got])
+        opt.finished()
         return results
