@@ -138,6 +138,8 @@ typedef struct {
   void *stream;          /* hipStream_t, NULL = library stream */
   int trans_a;           /* 1: A stored transposed, [K][lda] */
   int trans_b;           /* 1: B stored transposed, [N][ldb] */
+  int stages;            /* pipeline depth (LDS stages), 0 = the kernel's default;
+                            xtc_hip_matmul_pipeline_depths lists the legal ones */
 } xtc_hip_matmul_desc;
 
 int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B,
@@ -220,6 +222,17 @@ int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance *out);
 /* Tile the library picks when a descriptor leaves `tile` zeroed. */
 int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile *out,
                          int *split_k);
+
+/* Pipeline depths the kernel that runs `desc` (with 256-byte aligned
+ * operands) is compiled for: the LDS stages of the LDS-DMA kernels, 2 for
+ * the register-staged generic template, 1 for the scalar kernel.  Writes up
+ * to max_depths of them, the default first, and returns their count (-1 on
+ * error).  A schedule's unroll of the K-slab loop selects one
+ * (MlirCompilerPasses.py:579-596 unrolls loops by the scheduled factor; here
+ * the factor of the loop that walks the LDS slabs is how many slabs are in
+ * flight).  The conv2d kernels are compiled for one depth each. */
+int xtc_hip_matmul_pipeline_depths(const xtc_hip_matmul_desc *desc, int *depths, int max_depths);
+int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc *desc, int *depths, int max_depths);
 
 /* ---------------------------------------------------------- timing harness */
 

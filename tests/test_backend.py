@@ -152,7 +152,7 @@ def test_operand_layouts_lower_to_transpose_flags(tmp_path):
     assert ln.attrs["trans_a"] and ln.attrs["trans_b"] and (ln.attrs["M"], ln.attrs["N"], ln.attrs["K"]) == (4, 32, 512)
     module = backend.get_compiler(dump_file=str(tmp_path / "ml")).compile(backend.get_scheduler().schedule())
     # the two flags close the descriptor initializer (fields trans_a, trans_b)
-    assert re.search(r"xtc_hip_matmul_desc d = \{.*, 1, 1\};", module.source)
+    assert re.search(r"xtc_hip_matmul_desc d = \{.*, 1, 1, 0\};", module.source)
     natural = Backend(_matmul(4, 32, 512)).plan.launches[0].attrs
     assert not natural["trans_a"] and not natural["trans_b"]
 
@@ -364,6 +364,82 @@ def test_mapping_split_k():
     attrs, s = _sched(_matmul(256, 256, 1000), {"k": {"k1": 300}}, parallel=["k"])
     with pytest.raises(ScheduleError, match="multiple"):
         map_gemm(attrs, False, s, "nearest")
+
+
+def test_mapping_unroll_of_the_slab_loop_selects_the_pipeline_depth():
+    from xtc_amd.backends.hip.mapping import pipeline_depths
+
+    g = _matmul(4096, 4096, 4096)
+    tiles = {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 32}}
+
+    def cfg(t, unroll, parallel=None, graph=g):
+        b = Backend(graph)
+        sch = b.get_scheduler()
+        for d, v in t.items():
+            sch.tile(d, v)
+        if parallel:
+            sch.parallelize(parallel)
+        sch.unroll(unroll)
+        (ln,) = [l for l in b.plan.launches if l.kind == "matmul"]
+        return map_gemm(ln.attrs, False, sch.schedule().node(ln.node), "strict"), ln.attrs
+
+    # LDS-DMA fp32 256x128x32: 3 stages (default) or 2
+    c, attrs = cfg(tiles, {"k": 2})
+    assert c.tile == (256, 128, 32, 4, 2) and c.stages == 2
+    assert pipeline_depths(attrs, False, c.tile, 1) == [3, 2]
+    assert cfg(tiles, {"k": 3})[0].stages == 0  # the default depth is left to the kernel
+    with pytest.raises(ScheduleError, match=r"4-slab pipeline.*\[3, 2\]"):
+        cfg(tiles, {"k": 4})
+    # unroll of the MFMA loop inside a slab, or of M/N loops, is recorded only
+    assert cfg(tiles, {"k1": 32, "i1": 256})[0].stages == 0
+    # BK 16: 3-6 stages of 24 KB
+    t16 = {**tiles, "k": {"k1": 16}}
+    assert [cfg(t16, {"k": d})[0].stages for d in (3, 5, 6)] == [3, 5, 6]
+    # split-K: the slab loop is k1 (k is the parallel loop over splits)
+    tsk = {"i": {"i1": 128, "i2": 64}, "j": {"j1": 128, "j2": 32}, "k": {"k1": 2048, "k2": 32}}
+    c, _ = cfg(tsk, {"k1": 4}, parallel=["i", "j", "k"])
+    assert (c.split_k, c.stages) == (2, 4)
+    # the generic template double-buffers: depth 2 only
+    tg = {"i": {"i1": 64, "i2": 32}, "j": {"j1": 64, "j2": 32}, "k": {"k1": 32}}
+    assert cfg(tg, {"k": 2})[0].stages == 0
+    with pytest.raises(ScheduleError, match="pipeline"):
+        cfg(tg, {"k": 3})
+    # bf16 ping-pong 256x256x32: 4 (default), 3, 5
+    g3 = _matmul(8192, 8192, 8192, "bfloat16", out_dtype="float32")
+    tp = {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}
+    assert [cfg(tp, {"k": d}, graph=g3)[0].stages for d in (3, 4, 5)] == [3, 0, 5]
+
+
+def test_mapping_vectorize_checks_the_vector_width():
+    g = _matmul(4096, 4096, 4096)
+    b = Backend(g)
+    sch = b.get_scheduler()
+    sch.tile("i", {"i1": 256, "i2": 64})
+    sch.tile("j", {"j1": 128, "j2": 64, "j3": 2})
+    sch.tile("k", {"k1": 32})
+    sch.vectorize(["j2"])
+    (ln,) = b.plan.launches
+    assert map_gemm(ln.attrs, False, sch.schedule().node(ln.node), "strict").exact
+    sch.vectorize(["j3"])
+    with pytest.raises(ScheduleError, match=r"vectorize\(j3\): extent 2 .* 4-element"):
+        map_gemm(ln.attrs, False, sch.schedule().node(ln.node), "strict")
+
+
+def test_pipeline_depth_queries():
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_BF16, M=16, N=8192, K=8192, tile=capi.Tile(16, 128, 64, 1, 4), split_k=8)
+    assert capi.matmul_pipeline_depths(d) == [4, 3, 2]  # skinny bf16
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32, M=100, N=60, K=30)
+    assert capi.matmul_pipeline_depths(d) == [1]  # K and N not multiples of the 4-element vector: scalar kernel
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32, M=512, N=512, K=512, tile=capi.Tile(32, 32, 16, 1, 1), split_k=4)
+    assert capi.matmul_pipeline_depths(d) == [4]  # split-wave register ring
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_BF16, M=512, N=512, K=512, tile=capi.Tile(256, 256, 32, 2, 4), trans_b=1)
+    assert capi.matmul_pipeline_depths(d) == [4, 3, 5]  # B^T read natively by the ping-pong kernel
+    c = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=8, H=56, W=56, C=64, F=64, R=3, S=3, stride_h=1, stride_w=1,
+                        pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)
+    assert capi.conv2d_pipeline_depths(c) == [3]  # direct conv: 3 weight-tap stages
+    d = capi.MatmulDesc(dtype=7, M=1, N=1, K=1)
+    with pytest.raises(capi.HipError, match="bad dtype"):
+        capi.matmul_pipeline_depths(d)
 
 
 def test_mapping_column_major_raster():

@@ -10,6 +10,7 @@ import json
 
 import pytest
 
+from xtc_amd.backends.hip import Backend
 from xtc_amd.backends.hip.mapping import map_gemm
 from xtc_amd.cli.explore import DEFAULT_DIMS, build_graph
 from xtc_amd.search.explore import Exploration, ExplorationConfig, hip_sample_filter, parse_x
@@ -47,11 +48,11 @@ def test_run_writes_csv_db_manifest_and_resumes(tmp_path, monkeypatch):
     res = Exploration(g, cfg).run()
     assert len(res) == 5 and all(code == 0 for _, _, code, _ in res)
     rows = list(csv.DictReader(open(out)))
-    assert list(rows[0]) == ["bm", "wm", "bn", "wn", "bk", "split_k", "X", "time", "peak", "backend"]
+    assert list(rows[0]) == ["bm", "wm", "bn", "wn", "bk", "split_k", "stages", "X", "time", "peak", "backend"]
     assert len(rows) == 5 and all(float(r["time"]) == 1e-3 for r in rows)
     # peak = ops_count / peak_flops / time
     assert float(rows[0]["peak"]) == pytest.approx(512**3 / 1e12 / 1e-3)
-    assert all(r["X"].count(";") == 5 and "," not in r["X"] for r in rows)
+    assert all(r["X"].count(";") == 6 and "," not in r["X"] for r in rows)
     db = [json.loads(l) for l in open(tmp_path / "r.jsonl")]
     assert len(db) == 5 and all(d["kernels"]["C"].startswith("gemm<float32>") for d in db)
     # results-DB record of the reference (callback.py:46-60, query_results.py:78-123)
@@ -62,12 +63,18 @@ def test_run_writes_csv_db_manifest_and_resumes(tmp_path, monkeypatch):
     assert d["strategy"][0] == "xtc.strategy" and d["strategy"][2] == "tile_hip"
     assert [x["schedule"] for x in db] == [parse_x(r["X"]) for r in rows]
     meta = json.loads((tmp_path / "r.csv.meta.json").read_text())
-    assert meta["sampleNames"] == ["bm", "wm", "bn", "wn", "bk", "split_k"] and meta["args"]["trials"] == 5
-    # every sampled schedule compiled to exactly the kernel it names
+    assert meta["sampleNames"] == ["bm", "wm", "bn", "wn", "bk", "split_k", "stages"] and meta["args"]["trials"] == 5
+    # every sampled schedule compiled to exactly the kernel it names, at the
+    # pipeline depth it names (0 in the config = the kernel's default depth)
+    from xtc_amd.backends.hip.mapping import pipeline_depths
+
+    (ln,) = Backend(g).plan.launches
     for sample, conf in zip([parse_x(r["X"]) for r in rows], calls):
         (c,) = conf.values()
-        bm, wm, bn, wn, bk, sk = sample
+        bm, wm, bn, wn, bk, sk, st = sample
         assert (c.bm, c.bn, c.bk, c.bm // c.wgm, c.bn // c.wgn, c.split_k, c.exact) == (bm, bn, bk, wm, wn, sk, True)
+        default = pipeline_depths(ln.attrs, False, c.tile, sk)[0]
+        assert c.stages == (0 if st == default else st)
     # resume: the same samples are not run again
     calls.clear()
     cfg.resume = True

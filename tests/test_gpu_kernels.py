@@ -735,3 +735,72 @@ def test_direct_conv_is_the_default_for_c4_and_strided_falls_back():
     out = run_conv(x, wt, stride=(2, 2), pads=(1, 1, 1, 1), tile=DIRECT)
     xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
     np.testing.assert_array_equal(out, ref.conv2d(xp, wt, (2, 2)).astype(np.float32))
+
+
+# ------------------------------------------------------------------ pipeline depths
+
+# (dtype, tile, split_k, (M, N, K), trans_b): every kernel with more than one
+# compiled pipeline depth, at slab counts below, at and above the depths
+DEPTH_CASES = [
+    ("float32", (256, 128, 16, 4, 2), 1, (512, 256, 512), False),
+    ("float32", (256, 128, 16, 4, 2), 1, (256, 128, 48), False),
+    ("float32", (128, 256, 16, 2, 4), 1, (256, 512, 160), False),
+    ("float32", (256, 128, 32, 4, 2), 1, (512, 256, 64), False),
+    ("float32", (128, 256, 32, 2, 4), 1, (256, 512, 512), False),
+    ("float32", (128, 128, 32, 2, 4), 2, (256, 256, 1024), False),
+    ("float32", (128, 128, 32, 2, 4), 1, (128, 128, 32), False),
+    ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 512, 32), False),
+    ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 512, 160), False),
+    ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 512, 1056), False),
+    ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 256, 224), True),
+    ("bfloat16", (16, 128, 64, 1, 4), 8, (16, 1024, 8192), False),
+    ("bfloat16", (16, 128, 64, 1, 4), 8, (12, 1024, 4096), False),
+]
+
+
+def _run_depth(a, b, dtype, tile, split_k, stages, trans_b):
+    M, K = a.shape
+    N = b.shape[1]
+    A = _dev(a, dtype)
+    B = _dev(np.ascontiguousarray(b.T) if trans_b else b, dtype)
+    C = DeviceBuffer(M * N * 4)
+    d = capi.MatmulDesc()
+    d.dtype = capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16
+    d.M, d.N, d.K = M, N, K
+    d.tile = capi.Tile(*tile)
+    d.split_k = split_k
+    d.xcd_remap = 1
+    d.trans_b = int(trans_b)
+    d.stages = stages
+    L = capi.lib()
+    capi.check(L.xtc_hip_matmul(ctypes.byref(d), A.c_ptr, B.c_ptr, C.c_ptr, None), "matmul")
+    capi.check(L.xtc_hip_synchronize(), "sync")
+    return C.to_numpy((M, N), np.float32)
+
+
+@pytest.mark.parametrize("case", DEPTH_CASES, ids=[f"{c[0]}-{c[1]}-sk{c[2]}-{c[3]}{'-bt' if c[4] else ''}"
+                                                   for c in DEPTH_CASES])
+def test_every_pipeline_depth(case):
+    dtype, tile, split_k, (M, N, K), trans_b = case
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, M=M, N=N, K=K,
+                        tile=capi.Tile(*tile), split_k=split_k, trans_b=int(trans_b))
+    depths = capi.matmul_pipeline_depths(d)
+    assert len(depths) > 1, depths
+    ai, bi = ref.np_init((M, K), "float32"), ref.np_init((K, N), "float32")
+    want_int = ref.matmul(ai, bi).astype(np.float32)
+    ar, br = rng_uniform(11, (M, K)), rng_uniform(12, (K, N))
+    if dtype == "bfloat16":
+        ar, br = ref.round_bf16(ar), ref.round_bf16(br)
+    default = _run_depth(ar, br, dtype, tile, split_k, 0, trans_b)
+    err = ref.scaled_error(default, ref.matmul(ar, br), K, np.abs(ar).max(), np.abs(br).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+    for depth in depths:
+        print(f"[depth] {depth}", flush=True)
+        np.testing.assert_array_equal(_run_depth(ai, bi, dtype, tile, split_k, depth, trans_b), want_int)
+        np.testing.assert_array_equal(_run_depth(ar, br, dtype, tile, split_k, depth, trans_b), default)
+
+
+def test_unsupported_pipeline_depth_is_an_error():
+    a, b = rng_uniform(1, (512, 64)), rng_uniform(2, (64, 256))
+    with pytest.raises(capi.HipError, match=r"pipeline depths \{3, 2\}, not 5"):
+        _run_depth(a, b, "float32", (256, 128, 32, 4, 2), 1, 5, False)

@@ -17,10 +17,22 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
                                         the second k level
   * interchange with N's base loop outside M's -> column-major tile raster;
     otherwise tiles are rastered in groups of 8 tile-rows (L2 reuse)
-  * vectorize, unroll, pack_at(local), buffer_at, fuse_producer_at -> always
-    on in these kernels (16-byte vector loads, fully unrolled MFMA loops,
-    LDS staging of both operands, register-resident output tile, pad folded
-    into the conv loader); recorded, no further effect.
+  * unroll of the loop that walks the K slabs (k without split-K, k1 with
+    it; c for conv) by S -> pipeline depth S: S slabs in flight through S
+    LDS stages.  It must be a depth the kernel is compiled for
+    (xtc_hip_matmul_pipeline_depths: 3-6 for the fp32 LDS-DMA BK-16 tiles,
+    2-3 for its BK-32 256-wide tiles, 2-4 for 128x128, 3-5 for the bf16
+    ping-pong kernel, 2-4 for the skinny bf16 kernel, 2 for the generic
+    template); absent, the kernel's default.  Unroll factors of the other
+    loops are recorded: the MFMA loop over a slab and the wave's sub-tiles
+    are always fully unrolled, and the block and wave tiles are spread over
+    waves and lanes
+  * vectorize(loop) -> the 16-byte loads and stores of every kernel (4 fp32
+    or 8 bf16 elements): the vectorized loop's extent must be a multiple of
+    that width, or the schedule is rejected
+  * pack_at(local), buffer_at, fuse_producer_at -> always on in these
+    kernels (LDS staging of both operands, register-resident output tile,
+    pad folded into the conv loader); recorded, no further effect.
 
 Tile semantics follow the reference: a tile size is the extent of the
 sub-loop (src/xtc/backends/mlir/MlirCompilerPasses.py:414-457).
@@ -42,7 +54,7 @@ from typing import Any
 
 from .scheduler import HipNodeSchedule, ScheduleError
 
-__all__ = ["GemmConfig", "map_gemm", "gemm_instances", "legal_tiles"]
+__all__ = ["GemmConfig", "map_gemm", "gemm_instances", "legal_tiles", "pipeline_depths"]
 
 DEFAULT_GROUP_M = 8
 
@@ -61,15 +73,17 @@ class GemmConfig:
     xcd_remap: int = 1
     exact: bool = True
     source: str = "schedule"  # "schedule" | "nearest" | "default"
+    stages: int = 0  # pipeline depth, 0 = the kernel's default
 
     @property
     def tile(self) -> tuple[int, int, int, int, int]:
         return (self.bm, self.bn, self.bk, self.wgm, self.wgn)
 
     def describe(self) -> str:
+        depth = f" stages={self.stages}" if self.stages else ""
         return (
             f"{'conv' if self.conv else 'gemm'}<{self.dtype}> BMxBNxBK={self.bm}x{self.bn}x{self.bk} "
-            f"waves={self.wgm}x{self.wgn} split_k={self.split_k} group_m={self.group_m} ({self.source})"
+            f"waves={self.wgm}x{self.wgn} split_k={self.split_k}{depth} group_m={self.group_m} ({self.source})"
         )
 
 
@@ -109,6 +123,72 @@ def _default(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[int,
     from ...runtimes.hip import capi
 
     return capi.default_tile(dtype, conv, M, N, K)
+
+
+def _attrs_key(attrs: dict[str, Any], conv: bool) -> tuple[Any, ...]:
+    if conv:
+        return (attrs["dtype"], attrs["NB"], attrs["H"], attrs["W"], attrs["C"], attrs["F"], attrs["R"], attrs["S"],
+                tuple(attrs["stride"]), tuple(attrs["pads"]))
+    return (attrs["dtype"], attrs["M"], attrs["N"], attrs["K"], bool(attrs.get("trans_a")),
+            bool(attrs.get("trans_b")))
+
+
+@lru_cache(maxsize=4096)
+def _depths(key: tuple[Any, ...], conv: bool, tile: tuple[int, int, int, int, int], split_k: int) -> tuple[int, ...]:
+    from ...runtimes.hip import capi
+
+    dt = capi.XTC_HIP_F32 if key[0] == "float32" else capi.XTC_HIP_BF16
+    if conv:
+        _, nb, h, w, c, f, r, s, (sh, sw), (pt, pb, pl, pr) = key
+        cd = capi.Conv2dDesc(dtype=dt, N=nb, H=h, W=w, C=c, F=f, R=r, S=s, stride_h=sh, stride_w=sw, pad_top=pt,
+                             pad_bottom=pb, pad_left=pl, pad_right=pr, tile=capi.Tile(*tile), split_k=split_k)
+        return tuple(capi.conv2d_pipeline_depths(cd))
+    _, m, n, k, ta, tb = key
+    md = capi.MatmulDesc(dtype=dt, M=m, N=n, K=k, tile=capi.Tile(*tile), split_k=split_k, trans_a=int(ta),
+                         trans_b=int(tb))
+    return tuple(capi.matmul_pipeline_depths(md))
+
+
+def pipeline_depths(attrs: dict[str, Any], conv: bool, tile: tuple[int, int, int, int, int], split_k: int) -> list[int]:
+    """Pipeline depths of the kernel that runs this launch with `tile` and
+    `split_k`, its default first (xtc_hip_*_pipeline_depths)."""
+    return list(_depths(_attrs_key(attrs, conv), conv, tuple(tile), int(split_k)))
+
+
+def _slab_loop(sched: HipNodeSchedule, k_dims: list[str], split: bool) -> str:
+    """Name of the loop that walks the K slabs: the loop just outside the
+    slab level (the K dim itself without split-K, its first tile level with
+    it; for conv, the innermost reduction dim c)."""
+    dim = k_dims[-1]
+    names = list(sched.tiles.get(dim, {}))
+    return names[0] if split and names else dim
+
+
+def _requested_depth(sched: HipNodeSchedule, k_dims: list[str], split: bool) -> int | None:
+    from ...itf.schd import DEFAULT_ROOT
+    from .scheduler import loop_name
+
+    return sched.unrolling.get(loop_name(DEFAULT_ROOT, _slab_loop(sched, k_dims, split)))
+
+
+def _check_vectorize(sched: HipNodeSchedule, dtype: str) -> None:
+    from .scheduler import basename
+
+    width = 4 if dtype == "float32" else 8
+    for qualified in sched.vectorization:
+        name = basename(qualified)
+        extent = None
+        if name in sched.dims:
+            extent = sched.sizes.get(name)
+        else:
+            for levels in sched.tiles.values():
+                if name in levels:
+                    extent = levels[name]
+        if extent is not None and extent % width:
+            raise ScheduleError(
+                f"{sched.node_name}: vectorize({name}): extent {extent} is not a multiple of the {width}-element "
+                f"(16-byte) vectors the {dtype} kernels load and store"
+            )
 
 
 def _nearest(req: dict[str, int | None], cands: list[tuple[int, int, int, int, int]]) -> tuple[int, int, int, int, int]:
@@ -174,10 +254,25 @@ def map_gemm(
         and (wm is None or t[0] // t[3] == wm)
         and (wn is None or t[1] // t[4] == wn)
     ]
+    _check_vectorize(sched, dtype)
+    depth = _requested_depth(sched, k_dims, k_parallel)
     if matches:
         # unspecified wave split: the instance with the most waves
         tile = max(matches, key=lambda t: (t[3] * t[4], t[3]))
-        return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=True, source="schedule")
+        stages = 0
+        if depth is not None:
+            depths = pipeline_depths(launch_attrs, conv, tile, split_k)
+            if depth not in depths:
+                if policy == "strict":
+                    raise ScheduleError(
+                        f"{sched.node_name}: unroll({_slab_loop(sched, k_dims, k_parallel)}: {depth}) asks for a "
+                        f"{depth}-slab pipeline; the kernel of tile {tile} runs {depths} (default {depths[0]})"
+                    )
+                return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=False,
+                                  source="nearest")
+            stages = 0 if depth == depths[0] else depth
+        return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=True, source="schedule",
+                          stages=stages)
     if policy == "strict":
         wave = "" if wm is None and wn is None else f" wave tile {wm}x{wn}"
         raise ScheduleError(

@@ -570,6 +570,42 @@ void launch_f32_lds(const GemmArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((gemm_f32_lds<BM, BN, BK, WGM, WGN, STAGES>), grid, dim3(512), 0, s, a);
 }
 
+// Compiled pipeline depths (LDS stages) of the LDS-DMA fp32 kernel, per tile;
+// the first entry of a tile is its default.  BK 16 stages are 24 KB (up to
+// 6 fit), BK 32 stages 48 KB for the 256-wide tiles (up to 3) and 32 KB for
+// 128x128 (up to 4: five would leave no room for the split-K flag).  Against 3 stages of BK 32, 4-5 stages of BK 16
+// measured 2-4 % faster on one box and 1-1.5 % slower on another.
+struct F32LdsVariant {
+  int bm, bn, bk, wgm, wgn, stages;
+  GemmLaunch launch;
+};
+const F32LdsVariant kF32Lds[] = {
+    {256, 128, 16, 4, 2, 4, &launch_f32_lds<256, 128, 16, 4, 2, 4>},
+    {256, 128, 16, 4, 2, 3, &launch_f32_lds<256, 128, 16, 4, 2, 3>},
+    {256, 128, 16, 4, 2, 5, &launch_f32_lds<256, 128, 16, 4, 2, 5>},
+    {256, 128, 16, 4, 2, 6, &launch_f32_lds<256, 128, 16, 4, 2, 6>},
+    {128, 256, 16, 2, 4, 5, &launch_f32_lds<128, 256, 16, 2, 4, 5>},
+    {128, 256, 16, 2, 4, 3, &launch_f32_lds<128, 256, 16, 2, 4, 3>},
+    {128, 256, 16, 2, 4, 4, &launch_f32_lds<128, 256, 16, 2, 4, 4>},
+    {128, 256, 16, 2, 4, 6, &launch_f32_lds<128, 256, 16, 2, 4, 6>},
+    {256, 128, 32, 4, 2, 3, &launch_f32_lds<256, 128, 32, 4, 2, 3>},
+    {256, 128, 32, 4, 2, 2, &launch_f32_lds<256, 128, 32, 4, 2, 2>},
+    {128, 256, 32, 2, 4, 3, &launch_f32_lds<128, 256, 32, 2, 4, 3>},
+    {128, 256, 32, 2, 4, 2, &launch_f32_lds<128, 256, 32, 2, 4, 2>},
+    {128, 128, 32, 2, 4, 3, &launch_f32_lds<128, 128, 32, 2, 4, 3>},
+    {128, 128, 32, 2, 4, 2, &launch_f32_lds<128, 128, 32, 2, 4, 2>},
+    {128, 128, 32, 2, 4, 4, &launch_f32_lds<128, 128, 32, 2, 4, 4>},
+};
+
+// The variant of tile t with `stages` (0: the tile's default), or null.
+const F32LdsVariant* f32_lds_variant(const xtc_hip_tile& t, int stages) {
+  for (const F32LdsVariant& v : kF32Lds)
+    if (v.bm == t.bm && v.bn == t.bn && v.bk == t.bk && v.wgm == t.wgm && v.wgn == t.wgn &&
+        (stages == 0 || v.stages == stages))
+      return &v;
+  return nullptr;
+}
+
 // The split-wave fp32 kernel (gemm_f32_splitwave.hpp) implements the
 // one-wave 32x32x16 tile with split-K 2..8 when the shape is aligned: the
 // splits of a tile are the waves of one workgroup instead of workgroups of
@@ -628,7 +664,7 @@ int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, in
   return 0;
 }
 
-int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
+int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int stages, int lda, int ldb, int ldc,
                        const void* A, const void* B, float* C, const float* bias, Scratch& x) {
   const hipStream_t s = x.s;
   const int splits = split_k < 1 ? 1 : split_k;
@@ -659,10 +695,22 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int l
     if (!a.counters) return 1;
   }
   dim3 grid((unsigned)(a.nblocks * splits));
-  if (d.K / splits == 1024)
+  const bool kc1024 = d.K / splits == 1024;
+  const int st = stages ? stages : 4;
+  if (kc1024 && st == 4)
     hipLaunchKernelGGL((gemm_bf16_skinny<1024, 4>), grid, dim3(256), 0, s, a);
-  else
+  else if (kc1024 && st == 3)
+    hipLaunchKernelGGL((gemm_bf16_skinny<1024, 3>), grid, dim3(256), 0, s, a);
+  else if (kc1024 && st == 2)
+    hipLaunchKernelGGL((gemm_bf16_skinny<1024, 2>), grid, dim3(256), 0, s, a);
+  else if (!kc1024 && st == 4)
     hipLaunchKernelGGL((gemm_bf16_skinny<512, 4>), grid, dim3(256), 0, s, a);
+  else if (!kc1024 && st == 3)
+    hipLaunchKernelGGL((gemm_bf16_skinny<512, 3>), grid, dim3(256), 0, s, a);
+  else if (!kc1024 && st == 2)
+    hipLaunchKernelGGL((gemm_bf16_skinny<512, 2>), grid, dim3(256), 0, s, a);
+  else
+    return fail("skinny bf16 kernel: no %d-stage pipeline", st);
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -718,7 +766,7 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, int OH, int OW, const void*
   return 0;
 }
 
-int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int lda, int ldb,
+int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int stages, int lda, int ldb,
                         int ldc, const void* A, const void* B, float* C, const float* bias,
                         hipStream_t s, bool bt) {
   BigGemmArgs a;
@@ -739,11 +787,24 @@ int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int
   a.group_m = d.group_m > 0 ? d.group_m : 8;  // 8 <= 16 at 8192^3, zero and random data
   a.xcd_remap = d.xcd_remap;
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (t.bk == 32) {  // 2x4 waves: the ping-pong schedule
-    if (bt)
+  if (t.bk == 32) {  // 2x4 waves: the ping-pong schedule, 3-5 stages of 32 KB
+    const int st = stages ? stages : 4;
+    if (bt && st == 4)
       hipLaunchKernelGGL((gemm_bf16_pingpong<true, 4>), grid, dim3(512), 0, s, a);
-    else
+    else if (!bt && st == 4)
       hipLaunchKernelGGL((gemm_bf16_pingpong<false, 4>), grid, dim3(512), 0, s, a);
+    else if (bt && st == 3)
+      hipLaunchKernelGGL((gemm_bf16_pingpong<true, 3>), grid, dim3(512), 0, s, a);
+    else if (!bt && st == 3)
+      hipLaunchKernelGGL((gemm_bf16_pingpong<false, 3>), grid, dim3(512), 0, s, a);
+    else if (bt && st == 5)
+      hipLaunchKernelGGL((gemm_bf16_pingpong<true, 5>), grid, dim3(512), 0, s, a);
+    else if (!bt && st == 5)
+      hipLaunchKernelGGL((gemm_bf16_pingpong<false, 5>), grid, dim3(512), 0, s, a);
+    else
+      return fail("ping-pong bf16 kernel: no %d-stage pipeline", st);
+  } else if (stages != 0 && stages != 2) {
+    return fail("256x256x64 bf16 kernel: no %d-stage pipeline", stages);
   } else if (t.wgm == 2) {
     if (bt)
       hipLaunchKernelGGL((gemm_bf16_256x256<2, 4, 64, 2, true>), grid, dim3(512), 0, s, a);
@@ -806,32 +867,151 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
   return dst;
 }
 
+// The kernel family a matmul runs on, chosen from the shape, tile, split,
+// strides and operand alignment in the order of matmul_impl.
+enum class MatmulPath { LdsDmaBt, Naive, LdsDma, Skinny, SplitWave, F32Lds, Generic };
+
+const char* path_name(MatmulPath p) {
+  switch (p) {
+    case MatmulPath::LdsDmaBt:
+    case MatmulPath::LdsDma:
+      return "LDS-DMA bf16";
+    case MatmulPath::Naive:
+      return "scalar";
+    case MatmulPath::Skinny:
+      return "skinny bf16";
+    case MatmulPath::SplitWave:
+      return "split-wave fp32";
+    case MatmulPath::F32Lds:
+      return "LDS-DMA fp32";
+    default:
+      return "generic";
+  }
+}
+
+// Pipeline depths the kernel of path p compiles for tile t: LDS stages of
+// the LDS-DMA kernels, the register-staged double buffer (2) of the generic
+// template, the split-wave kernel's ring of 4 register chunks, 1 for the
+// scalar kernel.  out[0] is the default.  Returns the count.
+int path_depths(MatmulPath p, const xtc_hip_tile& t, int* out, int max) {
+  int tmp[16];
+  int n = 0;
+  switch (p) {
+    case MatmulPath::LdsDmaBt:
+    case MatmulPath::LdsDma:
+      if (t.bk == 32) {
+        tmp[n++] = 4;
+        tmp[n++] = 3;
+        tmp[n++] = 5;
+      } else {
+        tmp[n++] = 2;
+      }
+      break;
+    case MatmulPath::Skinny:
+      tmp[n++] = 4;
+      tmp[n++] = 3;
+      tmp[n++] = 2;
+      break;
+    case MatmulPath::SplitWave:
+      tmp[n++] = 4;
+      break;
+    case MatmulPath::F32Lds:
+      for (const F32LdsVariant& v : kF32Lds)
+        if (v.bm == t.bm && v.bn == t.bn && v.bk == t.bk && v.wgm == t.wgm && v.wgn == t.wgn && n < 16)
+          tmp[n++] = v.stages;
+      break;
+    case MatmulPath::Naive:
+      tmp[n++] = 1;
+      break;
+    default:
+      tmp[n++] = 2;
+      break;
+  }
+  for (int i = 0; i < n && i < max; ++i) out[i] = tmp[i];
+  return n;
+}
+
+// 0 if `stages` (0 = default) is a depth of path p for tile t, else fails.
+int check_depth(MatmulPath p, const xtc_hip_tile& t, int stages) {
+  if (stages == 0) return 0;
+  int depths[16];
+  const int n = path_depths(p, t, depths, 16);
+  char list[96] = "";
+  for (int i = 0; i < n; ++i) {
+    if (depths[i] == stages) return 0;
+    const size_t used = strlen(list);
+    snprintf(list + used, sizeof(list) - used, i ? ", %d" : "%d", depths[i]);
+  }
+  return fail("the %s kernel for tile %dx%dx%d waves %dx%d has pipeline depths {%s}, not %d", path_name(p), t.bm,
+              t.bn, t.bk, t.wgm, t.wgn, list, stages);
+}
+
+// Strides, tile and split of descriptor d after defaults.  Returns 0, or
+// fails.
+int resolve_matmul(const xtc_hip_matmul_desc& d, int* lda, int* ldb, int* ldc, xtc_hip_tile* t, int* split_k) {
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
+  if (d.stages < 0) return fail("bad pipeline depth %d", d.stages);
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+  *lda = d.lda ? d.lda : (ta ? d.M : d.K);
+  *ldb = d.ldb ? d.ldb : (tb ? d.K : d.N);
+  *ldc = d.ldc ? d.ldc : d.N;
+  if (*lda < (ta ? d.M : d.K) || *ldb < (tb ? d.K : d.N) || *ldc < d.N)
+    return fail("leading dimension smaller than shape");
+  *t = d.tile;
+  *split_k = d.split_k;
+  if (t->bm == 0) {
+    int sk = 1;
+    default_tile(d.dtype, 0, d.M, d.N, d.K, t, &sk);
+    if (*split_k <= 0) *split_k = sk;
+  }
+  return 0;
+}
+
+// The path of a matmul whose operands, after any transposed copy, are A/B
+// with strides lda/ldb (the B^T-direct case is decided before the copies).
+int natural_path(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda, int ldb, int ldc,
+                 const void* A, const void* B, const void* C, const void* bias, MatmulPath* path) {
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 && aligned16(A) &&
+                      aligned16(B);
+  if (!vec_ok) {
+    *path = MatmulPath::Naive;
+    return 0;
+  }
+  if (!find_entry(d.dtype, 0, t))
+    return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype, t.bm, t.bn, t.bk, t.wgm,
+                t.wgn);
+  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, (const float*)bias, false))
+    *path = MatmulPath::LdsDma;
+  else if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, (const float*)bias))
+    *path = MatmulPath::Skinny;
+  else if (splitwave_gemm_applies(d, t, split_k, lda, A))
+    *path = MatmulPath::SplitWave;
+  else if (f32_lds_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, (const float*)bias))
+    *path = MatmulPath::F32Lds;
+  else
+    *path = MatmulPath::Generic;
+  return 0;
+}
+
 // xtc_hip_matmul with its scratch taken from `x` (whose stream is the
 // descriptor's).
 int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, float* C, const float* bias,
                 Scratch& x) {
   if (!A || !B || !C) return fail("null operand");
-  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
-  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
+  int lda, ldb, ldc, split_k;
+  xtc_hip_tile t;
+  if (resolve_matmul(d, &lda, &ldb, &ldc, &t, &split_k)) return 1;
   const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
-  int lda = d.lda ? d.lda : (ta ? d.M : d.K);
-  int ldb = d.ldb ? d.ldb : (tb ? d.K : d.N);
-  const int ldc = d.ldc ? d.ldc : d.N;
-  if (lda < (ta ? d.M : d.K) || ldb < (tb ? d.K : d.N) || ldc < d.N)
-    return fail("leading dimension smaller than shape");
   const hipStream_t s = x.s;
-  xtc_hip_tile t = d.tile;
-  int split_k = d.split_k;
-  if (t.bm == 0) {
-    int sk = 1;
-    default_tile(d.dtype, 0, d.M, d.N, d.K, &t, &sk);
-    if (split_k <= 0) split_k = sk;
-  }
   // B stored transposed feeds the LDS-DMA kernel directly (B^T tiles are
   // read like A tiles); every other transposed operand gets a natural copy
   // in a staging buffer first (one HBM-bound transpose).
-  if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true))
-    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, true);
+  if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true)) {
+    if (check_depth(MatmulPath::LdsDmaBt, t, d.stages)) return 1;
+    return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, true);
+  }
   const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
   if (ta) {
     A = transposed_copy(0, A, d.K, d.M, lda, esz, x);
@@ -843,10 +1023,10 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     if (!B) return 1;
     ldb = d.N;
   }
-  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
-  const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 &&
-                      aligned16(A) && aligned16(B);
-  if (!vec_ok) {
+  MatmulPath path;
+  if (natural_path(d, t, split_k, lda, ldb, ldc, A, B, C, bias, &path)) return 1;
+  if (check_depth(path, t, d.stages)) return 1;
+  if (path == MatmulPath::Naive) {
     dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
     if (d.dtype == XTC_HIP_F32)
       hipLaunchKernelGGL(gemm_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)A,
@@ -859,30 +1039,16 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     HIP_TRY(hipGetLastError());
     return 0;
   }
+  if (path == MatmulPath::LdsDma) return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, false);
+  if (path == MatmulPath::Skinny) return launch_skinny_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x);
+  if (path == MatmulPath::SplitWave) return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   const GemmEntry* e = find_entry(d.dtype, 0, t);
-  if (!e)
-    return fail("no matmul kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
-                t.bm, t.bn, t.bk, t.wgm, t.wgn);
-  if (lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, false))
-    return launch_lds_dma_gemm(d, t, lda, ldb, ldc, A, B, C, bias, s, false);
-  if (skinny_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias))
-    return launch_skinny_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, x);
-  if (splitwave_gemm_applies(d, t, split_k, lda, A))
-    return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
   GemmEntry lds_entry;
-  if (f32_lds_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias)) {
+  if (path == MatmulPath::F32Lds) {
     // same tiles, split-K set-up and grid as the generic instance; only the
     // kernel differs
     lds_entry = *e;
-    // BK 16 stages are 24 KB: 4 of them (256x128) or 5 (128x256).  Against
-    // 3 stages of BK 32 they measured 2-4 % faster on one box and 1-1.5 %
-    // slower on another, bit-identical
-    if (t.bk == 16)
-      lds_entry.launch = t.wgm == 4 ? &launch_f32_lds<256, 128, 16, 4, 2, 4> : &launch_f32_lds<128, 256, 16, 2, 4, 5>;
-    else
-      lds_entry.launch = t.wgm == 4    ? &launch_f32_lds<256, 128, 32, 4, 2, 3>
-                         : t.bn == 256 ? &launch_f32_lds<128, 256, 32, 2, 4, 3>
-                                       : &launch_f32_lds<128, 128, 32, 2, 4, 3>;
+    lds_entry.launch = f32_lds_variant(t, d.stages)->launch;
     e = &lds_entry;
   }
   GemmArgs a;
@@ -1115,6 +1281,48 @@ int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile*
   default_tile(dtype, conv, M, N, K, out, split_k);
   if (out->bm == 0) return fail("no kernel instance for dtype %d conv %d", dtype, conv);
   return 0;
+}
+
+int xtc_hip_matmul_pipeline_depths(const xtc_hip_matmul_desc* desc, int* depths, int max_depths) {
+  if (!desc || !depths || max_depths < 1) return -fail("null argument");
+  const xtc_hip_matmul_desc& d = *desc;
+  int lda, ldb, ldc, split_k;
+  xtc_hip_tile t;
+  if (resolve_matmul(d, &lda, &ldb, &ldc, &t, &split_k)) return -1;
+  // operands as the allocators hand them out: 256-byte aligned
+  const void* p = (const void*)(uintptr_t)256;
+  MatmulPath path;
+  if (d.trans_b && !d.trans_a && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, p, p, p, nullptr, true)) {
+    path = MatmulPath::LdsDmaBt;
+  } else {
+    if (d.trans_a) lda = d.K;
+    if (d.trans_b) ldb = d.N;
+    if (natural_path(d, t, split_k, lda, ldb, ldc, p, p, p, nullptr, &path)) return -1;
+  }
+  return path_depths(path, t, depths, max_depths);
+}
+
+int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths, int max_depths) {
+  if (!desc || !depths || max_depths < 1) return -fail("null argument");
+  const xtc_hip_conv2d_desc& d = *desc;
+  const int HP = d.H + d.pad_top + d.pad_bottom;
+  const int WP = d.W + d.pad_left + d.pad_right;
+  if (d.stride_h <= 0 || d.stride_w <= 0 || HP < d.R || WP < d.S) return -fail("bad conv2d descriptor");
+  const int OH = (HP - d.R) / d.stride_h + 1;
+  const int OW = (WP - d.S) / d.stride_w + 1;
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  if (d.C % vec || d.F % vec) {
+    depths[0] = 1;  // scalar kernel
+    return 1;
+  }
+  xtc_hip_tile t = d.tile;
+  int split_k = d.split_k;
+  if (t.bm == 0) default_tile(d.dtype, 1, d.N * OH * OW, d.F, d.R * d.S * d.C, &t, &split_k);
+  const void* p = (const void*)(uintptr_t)256;
+  // the direct kernel streams the weight taps through dconv::STAGES stages;
+  // the implicit-GEMM loader double-buffers through registers
+  depths[0] = direct_conv_applies(d, t, split_k, OH, OW, p, p, p, nullptr) ? dconv::STAGES : 2;
+  return 1;
 }
 
 int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B, float* C,

@@ -70,6 +70,7 @@ class MatmulDesc(ctypes.Structure):
         ("stream", ctypes.c_void_p),
         ("trans_a", ctypes.c_int),
         ("trans_b", ctypes.c_int),
+        ("stages", ctypes.c_int),
     ]
 
 
@@ -163,6 +164,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _i,
         [_i, _i, _i, _i, _i, ctypes.POINTER(Tile), ctypes.POINTER(_i)],
     ),
+    "xtc_hip_matmul_pipeline_depths": (_i, [ctypes.POINTER(MatmulDesc), ctypes.POINTER(_i), _i]),
+    "xtc_hip_conv2d_pipeline_depths": (_i, [ctypes.POINTER(Conv2dDesc), ctypes.POINTER(_i), _i]),
     "xtc_hip_evaluate_perf": (
         None,
         [
@@ -254,3 +257,21 @@ def default_tile(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[
     sk = ctypes.c_int(1)
     check(lib().xtc_hip_default_tile(_DTYPE_IDS[dtype], int(conv), M, N, K, ctypes.byref(t), ctypes.byref(sk)), "default_tile")
     return t.as_tuple(), int(sk.value)
+
+
+def matmul_pipeline_depths(desc: MatmulDesc) -> list[int]:
+    """Pipeline depths of the kernel that runs `desc`, the default first."""
+    out = (ctypes.c_int * 16)()
+    n = lib().xtc_hip_matmul_pipeline_depths(ctypes.byref(desc), out, 16)
+    if n < 0:
+        raise HipError(f"matmul_pipeline_depths: {last_error()}")
+    return list(out[: min(n, 16)])
+
+
+def conv2d_pipeline_depths(desc: Conv2dDesc) -> list[int]:
+    """Pipeline depths of the kernel that runs `desc`, the default first."""
+    out = (ctypes.c_int * 16)()
+    n = lib().xtc_hip_conv2d_pipeline_depths(ctypes.byref(desc), out, 16)
+    if n < 0:
+        raise HipError(f"conv2d_pipeline_depths: {last_error()}")
+    return list(out[: min(n, 16)])

@@ -42,13 +42,17 @@ from ..utils.math import factors_enumeration, factors_to_sizes
 __all__ = ["Strategies", "BaseStrategy", "BaseStrategyPRTScheme", "Strategy_HIP"]
 
 
-def _operation_of(graph: Any, node: str | None) -> Any:
+def _node_of(graph: Any, node: str | None) -> Any:
     if node is None:
-        return graph.outputs_nodes[0].operation
+        return graph.outputs_nodes[0]
     for n in graph.nodes.values():
         if n.name == node or n.uid == node:
-            return n.operation
+            return n
     raise ValueError(f"no node {node!r} in graph")
+
+
+def _operation_of(graph: Any, node: str | None) -> Any:
+    return _node_of(graph, node).operation
 
 
 class BaseStrategy(Strategy):
@@ -557,18 +561,21 @@ class Strategy_GOTO_R(Strategy_GOTO):
 class Strategy_HIP(BaseStrategy):
     """GPU space: every compiled GEMM kernel instance of the graph's dtype.
 
-    Sample [bm, wm, bn, wn, bk, split_k] (sizes, not factors); the mapping of
-    xtc_amd/backends/hip/mapping.py read backwards:
+    Sample [bm, wm, bn, wn, bk, split_k, stages] (sizes, not factors); the
+    mapping of xtc_amd/backends/hip/mapping.py read backwards:
       * matmul (i, j, k): tile(i, {i1: bm, i2: wm}), tile(j, {j1: bn, j2: wn}),
         and on k either {k1: bk} or, with split_k > 1, {k1: K/split_k, k2: bk}
         plus parallelize(k);
       * conv2d (b, h, w, f, r, s, c): the implicit-GEMM rows are b*h*w, so
         the block and wave heights are split over h and w (w takes up to 8),
-        f carries the block and wave widths and c the slab depth; split_k is 1.
+        f carries the block and wave widths and c the slab depth; split_k is 1;
+      * stages: unroll of the slab loop (k, or k1 under split-K; c for conv)
+        by the pipeline depth, one of the depths the tile's kernel is
+        compiled for on this shape (the default first).
     """
 
     def __init__(self, graph: Any, **kwargs: Any) -> None:
-        super().__init__(graph, ["bm", "wm", "bn", "wn", "bk", "split_k"], **kwargs)
+        super().__init__(graph, ["bm", "wm", "bn", "wn", "bk", "split_k", "stages"], **kwargs)
         dims = list(self._op.dims)
         kinds = [d for d in dims if d in self._op.dims_kind("R")]
         dtype = str(self._op.inputs_types[0].dtype)
@@ -587,6 +594,7 @@ class Strategy_HIP(BaseStrategy):
         else:
             raise ValueError("tile_hip applies to matmul (P, P, R) and conv2d (P, P, P, P, R, R, R) operations")
         self._dims = dims
+        self._attrs = self._launch_attrs(graph, _node_of(graph, kwargs.get("node")).name)
         tiles = sorted(set(legal_tiles(dtype, self._conv)))
         self._tiles = [t for t in tiles if t[0] <= max(16, self._M) * 2 and t[1] <= max(16, self._N) * 2]
         if self._conv:
@@ -596,13 +604,30 @@ class Strategy_HIP(BaseStrategy):
             self._splits = [s for s in (1, 2, 4, 8, 16) if s == 1 or (self._K % s == 0 and self._K // s >= 64)]
         self._dtype = dtype
 
+    @staticmethod
+    def _launch_attrs(graph: Any, node: str) -> dict[str, Any]:
+        """The HIP lowering's attributes of node `node`'s kernel launch."""
+        from ..backends.hip import Backend
+
+        for ln in Backend(graph).plan.launches:
+            if ln.kind in ("matmul", "conv2d") and ln.node == node:
+                return ln.attrs
+        raise ValueError(f"tile_hip: node {node} has no matmul/conv2d kernel launch")
+
+    def _depths(self, tile: tuple[int, int, int, int, int], split: int) -> list[int]:
+        from ..backends.hip.mapping import pipeline_depths
+
+        return pipeline_depths(self._attrs, self._conv, tile, split)
+
     def _points(self) -> list[list[int]]:
         out = []
-        for bm, bn, bk, wgm, wgn in self._tiles:
+        for tile in self._tiles:
+            bm, bn, bk, wgm, wgn = tile
             for s in self._splits:
                 if s > 1 and (self._K // s) % bk:
                     continue
-                out.append([bm, bm // wgm, bn, bn // wgn, bk, s])
+                for depth in self._depths(tile, s):
+                    out.append([bm, bm // wgm, bn, bn // wgn, bk, s, depth])
         return out
 
     def _independents(self) -> list[list[list[int]]]:
@@ -616,6 +641,7 @@ class Strategy_HIP(BaseStrategy):
 
     def _generate(self, sch: Any, in_x: list[int]) -> None:
         bm, wm, bn, wn, bk, split = in_x[:6]
+        depth = in_x[6] if len(in_x) > 6 else None
         if self._conv:
             b, h, w, f, r, s, c = self._dims
             w1, w2 = min(bm, 8), min(wm, 8)
@@ -625,6 +651,8 @@ class Strategy_HIP(BaseStrategy):
             sch.tile(f, {f"{f}1": bn, f"{f}2": wn})
             sch.tile(c, {f"{c}1": bk})
             sch.parallelize([b, h, w, f])
+            if depth is not None:
+                sch.unroll({c: depth})  # the slab loop: `depth` slabs in flight
             return
         i, j, k = self._dims
         sch.tile(i, {f"{i}1": bm, f"{i}2": wm})
@@ -633,16 +661,22 @@ class Strategy_HIP(BaseStrategy):
             sch.tile(k, {f"{k}1": self._K // split, f"{k}2": bk})
             sch.interchange([i, j, k, f"{i}1", f"{j}1", f"{k}1", f"{k}2", f"{i}2", f"{j}2"])
             sch.parallelize([i, j, k])
+            slab_loop = f"{k}1"
         else:
             sch.tile(k, {f"{k}1": bk})
             sch.interchange([i, j, k, f"{i}1", f"{j}1", f"{k}1", f"{i}2", f"{j}2"])
             sch.parallelize([i, j])
+            slab_loop = k
+        if depth is not None:
+            sch.unroll({slab_loop: depth})  # `depth` slabs in flight through LDS
 
     def _default_schedule(self, opt_level: int) -> list[int]:
         from ..runtimes.hip import capi
 
-        (bm, bn, bk, wgm, wgn), split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
-        return [bm, bm // wgm, bn, bn // wgn, bk, max(1, split)]
+        tile, split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
+        bm, bn, bk, wgm, wgn = tile
+        split = max(1, split)
+        return [bm, bm // wgm, bn, bn // wgn, bk, split, self._depths(tile, split)[0]]
 
 
 @dataclass
