@@ -133,6 +133,19 @@ def _xtc_protocol(cfg: str, backend, sch, dev, cargs, flops: int, dtype: str) ->
     return proto
 
 
+def _print_peaks() -> int:
+    """The measured MFMA peaks behind xtc_hip_evaluate_flops, as JSON lines."""
+    from xtc_amd.runtimes.hip.device import HipDevice
+
+    dev = HipDevice(0)
+    for dtype in ("float32", "bfloat16"):
+        for op in ("reference", "zero", "random"):
+            tf = 2 * dev.evaluate_flops(dtype, op) / 1e12
+            print(json.dumps({"mfma_peak": dtype, "operands": op, "tflops": round(tf, 1),
+                              "frac_of_datasheet": round(tf / PEAK_TFLOPS[dtype], 4)}), flush=True)
+    return 0
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -172,6 +185,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--no-protocol", action="store_true",
                     help="skip the evaluate_perf protocol pass (kernel traces then hold only the timed steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the measured MFMA ceiling")
+    ap.add_argument("--peak", action="store_true",
+                    help="only print the measured MFMA peaks (fp32, bf16; zero, random and the reference's operands)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
                     help="also time torch.matmul on the same inputs (matmul configs) and report it in config")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -179,6 +195,8 @@ def main(argv: list[str] | None = None) -> int:
     args = ap.parse_args(argv)
     if args.calibrate_copy:
         return _calibrate_copy(args.steps)
+    if args.peak:
+        return _print_peaks()
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU; a GEMM "
@@ -293,6 +311,17 @@ def main(argv: list[str] | None = None) -> int:
     if not args.no_protocol:
         print(f"[bench] {cfg}: evaluate_perf protocol", file=sys.stderr, flush=True)
         line["config"]["xtc_protocol"] = _xtc_protocol(cfg, backend, sch, dev, cargs, flops, dtype)
+    if not args.no_ceiling and cfg != "C3b":
+        # the measured MFMA ceiling (register-only MFMA loop, xtc_hip_evaluate_flops):
+        # on random operands the board's power limit holds it below the datasheet
+        print(f"[bench] {cfg}: measured MFMA ceiling", file=sys.stderr, flush=True)
+        ceil = {op: 2 * dev.evaluate_flops(dtype, op) / 1e12 for op in ("zero", "random")}
+        line["config"]["mfma_ceiling"] = {
+            "probe": "register-only MFMA loop, xtc_hip_evaluate_flops_operands",
+            "zero_tflops": round(ceil["zero"], 1),
+            "random_tflops": round(ceil["random"], 1),
+            "kernel_frac_of_random_ceiling": round(roof["achieved"] / ceil["random"], 4),
+        }
     if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
         line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup)
     if not args.no_cpu:

@@ -266,10 +266,26 @@ int xtc_hip_evaluate_status(void);
 void xtc_hip_evaluate(double *results, int repeat, int number, int min_repeat_ms,
                       void (*func)(void), void **args, int nargs);
 
-/* Peak multiply-accumulates per second of the device for dtype ("float32",
- * "bfloat16"): XTC counts one op per FMA (operation.py:76-82), so this is
- * half the FLOP/s figure.  0.0 for unsupported dtypes. */
+/* Measured peak multiply-accumulates per second of the current device for
+ * dtype ("float32", "bfloat16"), the device counterpart of the reference's
+ * evaluate_flops microbenchmark (evaluate_flops.c:431-494): a register-only
+ * loop of independent MFMAs (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16)
+ * on every CU, one wave per SIMD and two workgroups per CU, timed with events
+ * over three batches of five ~20 ms launches, best batch.  XTC counts one op
+ * per FMA (operation.py:76-82), so this is half the FLOP/s figure.  Operands
+ * are the reference's integers 1 + i % 127.  0.0 on error (no device,
+ * unsupported dtype; message in xtc_hip_last_error()). */
 double xtc_hip_evaluate_flops(const char *dtype);
+
+/* The same probe with operand pattern `operands`: 0 the integers 1 + i % 127,
+ * 1 zeros, 2 uniform [-1, 1) (bf16: rounded to nearest even).  Under the
+ * board's power limit the rate depends on the operands' switching activity:
+ * this is the ceiling a GEMM on such data can reach. */
+double xtc_hip_evaluate_flops_operands(const char *dtype, int operands);
+
+/* Published dense MFMA peak of MI355X for dtype, in FMA/s (fp32 157.3,
+ * bf16/fp16 2516.6, fp64 78.6 TFLOP/s halved); 0.0 for others. */
+double xtc_hip_datasheet_flops(const char *dtype);
 
 #ifdef __cplusplus
 }

@@ -129,10 +129,10 @@ def test_c3a_seeded_tuned_rows():
 # The schedules bench.py measures (xtc_amd.configs.SCHEDULES), each compiled
 # with the strict policy and checked on the seeded BASELINE inputs.
 BENCH_KERNELS = {
-    "C1": {"C": ((32, 32, 16, 1, 1), 4)},
-    "C2": {"C": ((256, 128, 32, 4, 2), 1)},
-    "C3a": {"C": ((256, 256, 32, 2, 4), 1)},
-    "C5": {"fc1": ((128, 256, 32, 2, 4), 1), "fc2": ((128, 128, 32, 2, 4), 2)},
+    "C1": {"C": ((32, 32, 16, 1, 1), 4, 0)},
+    "C2": {"C": ((128, 256, 32, 2, 4), 1, 2)},
+    "C3a": {"C": ((256, 256, 32, 2, 4), 1, 0)},
+    "C5": {"fc1": ((128, 256, 32, 2, 4), 1, 0), "fc2": ((128, 128, 32, 2, 4), 2, 0)},
 }
 
 
@@ -142,7 +142,7 @@ def _bench_module(cfg):
     backend = Backend(configs.graph(cfg))
     sch = configs.apply_schedule(backend.get_scheduler(), cfg)
     module = backend.get_compiler(schedule_policy="strict").compile(sch.schedule())
-    got = {node: (c.tile, c.split_k) for node, c in module.configs.items()}
+    got = {node: (c.tile, c.split_k, c.stages) for node, c in module.configs.items()}
     assert got == BENCH_KERNELS[cfg], got
     return module
 
@@ -330,3 +330,21 @@ def test_operand_layouts_seeded_logical_parameters():
                       tiles={"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 64}})
     (out,) = _run(module, [a, b])
     assert ref.scaled_error(out, ref.matmul(a, b), 1024, 1.0, 1.0) <= TOL_BF16
+
+
+def test_measured_mfma_peak():
+    # the register-only MFMA probe behind evaluate_flops (FMA/s): at most the
+    # datasheet peak, and zeros run at least as fast as random operands
+    from xtc_amd.runtimes.hip.device import HipDevice
+
+    dev = HipDevice(0)
+    for dtype in ("float32", "bfloat16"):
+        sheet = dev.datasheet_flops(dtype)
+        ref_ops = dev.evaluate_flops(dtype)
+        zero = dev.evaluate_flops(dtype, "zero")
+        rand = dev.evaluate_flops(dtype, "random")
+        print(f"[peak] {dtype}: reference operands {ref_ops / sheet:.3f}, zeros {zero / sheet:.3f}, "
+              f"random {rand / sheet:.3f} of the datasheet", flush=True)
+        for v in (ref_ops, zero, rand):
+            assert 0.4 * sheet < v <= 1.02 * sheet
+        assert zero >= 0.97 * rand

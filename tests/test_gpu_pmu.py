@@ -5,7 +5,8 @@ asks them of CUPTI.  rocprofiler-sdk accepts the counter tool only before
 the ROCm runtime starts, so each case runs in a fresh Python process.
 
 Pinned values: SQ_WAVES counts the waves a call launches, which the tile
-fixes (64 workgroups x 4 waves for 512^3 with 64x64 tiles and 2x2 waves);
+fixes (64 workgroups x 4 waves for 512^3 with 64x64 tiles and 2x2 waves,
+plus the single wave of the completion signal of xtc_hip_synchronize);
 gpu.cycles reads GRBM_GUI_ACTIVE (the same slot, the same value); an unknown
 counter reads -1, as the reference reports an event it cannot open.
 """
@@ -88,7 +89,9 @@ def test_gpu_counters_per_call():
         # counter collection serialises and instruments every dispatch, so
         # the device time per call is perturbed (ms, not the us of a plain run)
         assert 0 < t < 0.1
-        assert waves == 64 * 4
+        # 64 workgroups x 4 waves of the GEMM, plus the one wave of the
+        # completion signal that the payload's xtc_hip_synchronize queues
+        assert waves == 64 * 4 + 1
         assert cycles == gui and cycles > 0
         assert unknown == -1
 

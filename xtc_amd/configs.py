@@ -87,13 +87,15 @@ def inputs(cfg: str, g: Any) -> list[np.ndarray]:
 # Tuned schedules, written with XTC's scheduling primitives: the first tile
 # level of i/j is the workgroup tile, the second the wave tile, k's first
 # level the LDS slab; parallelize on k splits K (its first level is then the
-# slice per split, its second the slab).  The mapping onto kernel template
+# slice per split, its second the slab); unroll of the loop that walks the
+# slabs sets the pipeline depth (LDS stages).  The mapping onto kernel template
 # parameters is in xtc_amd/backends/hip/mapping.py.  Picked with
 # loop-explore --strategy tile_hip on MI355X; nodes without an entry keep the
 # library's default tile.
 SCHEDULES: dict[str, dict[str, dict[str, Any]]] = {
     "C3a": {"C": {"tile": {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}}},
-    "C2": {"C": {"tile": {"i": {"i1": 256, "i2": 64}, "j": {"j1": 128, "j2": 64}, "k": {"k1": 32}}}},
+    "C2": {"C": {"tile": {"i": {"i1": 128, "i2": 64}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}},
+                 "unroll": {"k": 2}}},
     "C1": {"C": {"tile": {"i": {"i1": 32, "i2": 32}, "j": {"j1": 32, "j2": 32}, "k": {"k1": 128, "k2": 16}},
                  "parallelize": ["i", "j", "k"]}},
     "C5": {

@@ -13,9 +13,11 @@
 #include <string.h>
 #include <time.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "gemm_bf16_lds.hpp"
 #include "gemm_bf16_skinny.hpp"
@@ -23,6 +25,7 @@
 #include "gemm_f32_splitwave.hpp"
 #include "gemm_f32_lds.hpp"
 #include "conv_direct.hpp"
+#include "mfma_peak.hpp"
 #include "registry.hpp"
 #include "xtc_hip.h"
 
@@ -72,8 +75,13 @@ struct StreamScratch {
 
 struct DeviceState {
   bool ready = false;
+  int cus = 0;  // compute units
   hipStream_t stream = nullptr;
   void* scratch_ptr = nullptr;  // this device's address of `scratch`
+  // completion word of the library stream in coherent host memory, and the
+  // last sequence number queued for it (xtc_hip_synchronize)
+  unsigned* done_flag = nullptr;
+  std::atomic<unsigned> done_seq{0};
   std::unordered_map<hipStream_t, StreamScratch> scratch;  // by launch stream
   std::string arch, name;
 };
@@ -238,6 +246,12 @@ bool zero_fill(void* p, size_t bytes, hipStream_t s) {
   hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n16 ? n16 : 1, 256)), dim3(256), 0, s, (uint4*)p, n16,
                      (unsigned char*)p + n16 * 16, ntail);
   return hipGetLastError() == hipSuccess;
+}
+
+// Release store of `v` to the host-visible completion word (xtc_hip_synchronize):
+// stream order puts it after every earlier launch of the stream.
+__global__ void stream_done_kernel(unsigned* flag, unsigned v) {
+  if (threadIdx.x == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __global__ void relu_kernel(const float* __restrict__ x, float* __restrict__ y, uint64_t n,
@@ -1092,8 +1106,11 @@ int xtc_hip_init(int device) {
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     HIP_TRY(hipGetSymbolAddress(&d.scratch_ptr, HIP_SYMBOL(scratch)));
+    HIP_TRY(hipHostMalloc((void**)&d.done_flag, 256, hipHostMallocCoherent));
+    *d.done_flag = 0;
     d.arch = prop.gcnArchName;
     d.name = prop.name;
+    d.cus = prop.multiProcessorCount;
     d.ready = true;
   }
   g_current = device;
@@ -1126,7 +1143,28 @@ void* xtc_hip_stream(void) {
 int xtc_hip_synchronize(void) {
   DeviceState* d = current_state();
   if (!d) return fail("xtc_hip_init not called");
-  HIP_TRY(hipStreamSynchronize(d->stream));
+  // A one-thread kernel queued behind the work stores the call's sequence
+  // number to coherent host memory, and the host spins on that word: the
+  // round trip is about 6 us where a stream synchronisation takes 11 us (the
+  // runtime's completion signal), which decides the time of short
+  // synchronous payloads.  The spin asks the stream itself every 50 us, so
+  // it also ends on completion without the store and on an error.
+  const unsigned seq = d->done_seq.fetch_add(1u) + 1u;
+  hipLaunchKernelGGL(stream_done_kernel, dim3(1), dim3(64), 0, d->stream, d->done_flag, seq);
+  if (hipGetLastError() != hipSuccess) {
+    HIP_TRY(hipStreamSynchronize(d->stream));
+    return 0;
+  }
+  double next_query = now_s() + 50e-6;
+  while ((int)(__atomic_load_n(d->done_flag, __ATOMIC_ACQUIRE) - seq) < 0) {
+    __builtin_ia32_pause();
+    if (now_s() >= next_query) {
+      const hipError_t e = hipStreamQuery(d->stream);
+      if (e == hipSuccess) break;
+      if (e != hipErrorNotReady) return fail("xtc_hip_synchronize: %s", hipGetErrorString(e));
+      next_query = now_s() + 50e-6;
+    }
+  }
   return 0;
 }
 
@@ -1678,7 +1716,7 @@ void xtc_hip_evaluate(double* results, int repeat, int number, int min_repeat_ms
   xtc_hip_evaluate_perf(results, 0, nullptr, repeat, number, min_repeat_ms, func, args, nargs);
 }
 
-double xtc_hip_evaluate_flops(const char* dtype) {
+double xtc_hip_datasheet_flops(const char* dtype) {
   // Published dense MFMA peaks of MI355X (256 CUs at 2.4 GHz), in FMA/s.
   if (!dtype) return 0.0;
   if (!strcmp(dtype, "float32")) return 157.3e12 / 2.0;
@@ -1686,5 +1724,89 @@ double xtc_hip_evaluate_flops(const char* dtype) {
   if (!strcmp(dtype, "float64")) return 78.6e12 / 2.0;
   return 0.0;
 }
+
+double xtc_hip_evaluate_flops_operands(const char* dtype, int operands) {
+  DeviceState* d = current_state();
+  if (!d) {
+    fail("evaluate_flops: xtc_hip_init not called");
+    return 0.0;
+  }
+  const bool bf16 = dtype && !strcmp(dtype, "bfloat16");
+  const bool f32 = dtype && !strcmp(dtype, "float32");
+  if ((!bf16 && !f32) || operands < 0 || operands > 2) {
+    fail("evaluate_flops: unsupported dtype %s or operands %d", dtype ? dtype : "(null)", operands);
+    return 0.0;
+  }
+  using namespace peak;
+  const int blocks = 2 * (d->cus > 0 ? d->cus : 256);
+  const size_t waves = (size_t)blocks * (kThreads / 64);
+  const size_t words = waves * 64 * (bf16 ? kBf16Frags * 8 : kF32Frags);  // bf16 halves or floats
+  // operand words: the reference's integers 1 + i % 127 (evaluate_flops.c:466-469),
+  // zeros, or uniform [-1, 1) from a fixed LCG (bf16: rounded to nearest even)
+  std::vector<uint16_t> h16(bf16 ? words : 0);
+  std::vector<float> h32(bf16 ? 0 : words);
+  uint64_t lcg = 0x9e3779b97f4a7c15ull;
+  for (size_t i = 0; i < words; ++i) {
+    float v = 0.f;
+    if (operands == 0) {
+      v = (float)(1 + i % 127);
+    } else if (operands == 2) {
+      lcg = lcg * 6364136223846793005ull + 1442695040888963407ull;
+      v = (float)((lcg >> 40) * (1.0 / 16777216.0)) * 2.f - 1.f;
+    }
+    if (bf16) {
+      unsigned u;
+      memcpy(&u, &v, 4);
+      h16[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else {
+      h32[i] = v;
+    }
+  }
+  const size_t in_bytes = words * (bf16 ? 2 : 4);
+  void *in = nullptr, *out = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  double best = 0.0;
+  // ~20 ms per launch at the datasheet rate
+  const int iters = bf16 ? 48000 : 12000;
+  const double fmas = (double)waves * iters * (bf16 ? kBf16FmaPerRound : kF32FmaPerRound);
+  auto launch = [&]() {
+    if (bf16)
+      hipLaunchKernelGGL(mfma_peak_bf16, dim3(blocks), dim3(kThreads), 0, d->stream, (const u32x4*)in,
+                         (float*)out, iters);
+    else
+      hipLaunchKernelGGL(mfma_peak_f32, dim3(blocks), dim3(kThreads), 0, d->stream, (const float*)in,
+                         (float*)out, iters);
+  };
+  bool ok = hipMalloc(&in, in_bytes) == hipSuccess && hipMalloc(&out, (size_t)blocks * kThreads * 4) == hipSuccess &&
+            hipMemcpyAsync(in, bf16 ? (const void*)h16.data() : (const void*)h32.data(), in_bytes,
+                           hipMemcpyHostToDevice, d->stream) == hipSuccess &&
+            hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess;
+  if (ok) {
+    launch();  // cold run
+    // three batches of 5 launches back to back (~100 ms each, long enough for
+    // the clock to settle at the power limit); the best batch's rate
+    for (int rep = 0; ok && rep < 3; ++rep) {
+      ok = hipEventRecord(e0, d->stream) == hipSuccess;
+      for (int l = 0; l < 5; ++l) launch();
+      ok = ok && hipGetLastError() == hipSuccess && hipEventRecord(e1, d->stream) == hipSuccess &&
+           hipEventSynchronize(e1) == hipSuccess;
+      float ms = 0.f;
+      ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms > 0.f;
+      if (ok && 5 * fmas / (ms * 1e-3) > best) best = 5 * fmas / (ms * 1e-3);
+    }
+  }
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  hipStreamSynchronize(d->stream);
+  if (in) hipFree(in);
+  if (out) hipFree(out);
+  if (!ok) {
+    fail("evaluate_flops: the MFMA probe failed");
+    return 0.0;
+  }
+  return best;
+}
+
+double xtc_hip_evaluate_flops(const char* dtype) { return xtc_hip_evaluate_flops_operands(dtype, 0); }
 
 }  // extern "C"

@@ -186,6 +186,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "xtc_hip_evaluate_status": (_i, []),
     "xtc_hip_evaluate_flops": (ctypes.c_double, [ctypes.c_char_p]),
+    "xtc_hip_evaluate_flops_operands": (ctypes.c_double, [ctypes.c_char_p, _i]),
+    "xtc_hip_datasheet_flops": (ctypes.c_double, [ctypes.c_char_p]),
 }
 
 _lib: ctypes.CDLL | None = None

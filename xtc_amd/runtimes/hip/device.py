@@ -195,10 +195,24 @@ class HipDevice(AcceleratorDevice):
     def cndarray_copy_to_data(self, handle: Any, data_handle: Any) -> None:
         raise NotImplementedError("use xtc_amd.runtimes.hip.ndarray.DeviceArray")
 
-    def evaluate_flops(self, dtype_name: str | bytes) -> float:
-        """Dense MFMA peak of MI355X in FMA/s (one XTC op per FMA)."""
+    OPERANDS = {"reference": 0, "zero": 1, "random": 2}
+
+    def evaluate_flops(self, dtype_name: str | bytes, operands: str = "reference") -> float:
+        """Measured MFMA peak of the device in FMA/s (one XTC op per FMA):
+        a register-only MFMA loop, operands the reference's integers
+        1 + i % 127 (evaluate_flops.c:466-469), "zero" or "random"."""
         name = dtype_name.decode() if isinstance(dtype_name, bytes) else dtype_name
-        return float(capi.lib().xtc_hip_evaluate_flops(name.encode()))
+        self.init_device()
+        L = capi.lib()
+        v = float(L.xtc_hip_evaluate_flops_operands(name.encode(), self.OPERANDS[operands]))
+        if v <= 0.0:
+            raise capi.HipError(capi.last_error() or f"evaluate_flops({name}) failed")
+        return v
+
+    @staticmethod
+    def datasheet_flops(dtype_name: str) -> float:
+        """Published dense MFMA peak of MI355X in FMA/s."""
+        return float(capi.lib().xtc_hip_datasheet_flops(dtype_name.encode()))
 
     def __repr__(self) -> str:
         return f"HipDevice({self._device})"
