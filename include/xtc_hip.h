@@ -223,6 +223,12 @@ int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance *out);
 int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile *out,
                          int *split_k);
 
+/* Tile a conv2d descriptor gets when it leaves `tile` zeroed.  Unlike
+ * xtc_hip_default_tile(dtype, 1, ...) it sees the window, strides and pads:
+ * the direct conv kernel's wider 8x14-pixel block (tile 112x64x16, 1x4
+ * waves) replaces the 8x8 one when its input halo fits. */
+int xtc_hip_conv2d_default_tile(const xtc_hip_conv2d_desc *desc, xtc_hip_tile *out, int *split_k);
+
 /* Pipeline depths the kernel that runs `desc` (with 256-byte aligned
  * operands) is compiled for: the LDS stages of the LDS-DMA kernels, 2 for
  * the register-staged generic template, 1 for the scalar kernel.  Writes up

@@ -276,9 +276,19 @@ def test_conv_stride_asym_pad_value(dtype):
 
 
 def test_every_conv_instance():
+    # tiles that exist only in the direct conv kernel (C and F multiples of
+    # 64) have no kernel for this shape; test_direct_conv_8x14_* cover them
     failures = []
     for inst in _instances(True):
         dtype = inst["dtype"]
+        probe = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, N=2, H=10, W=12,
+                                C=16, F=32, R=3, S=3, stride_h=1, stride_w=1, pad_top=1, pad_bottom=1, pad_left=1,
+                                pad_right=1, tile=capi.Tile(*inst["tile"]))
+        try:
+            capi.conv2d_pipeline_depths(probe)
+        except capi.HipError:
+            assert inst["tile"] == (112, 64, 16, 1, 4), inst
+            continue
         x = ref.np_init((2, 10, 12, 16), "float32")
         w = (ref.np_init((3, 3, 16, 32), "float32")[::-1]).copy()
         out = run_conv(x, w, dtype, pads=(1, 1, 1, 1), tile=inst["tile"])
@@ -804,3 +814,40 @@ def test_unsupported_pipeline_depth_is_an_error():
     a, b = rng_uniform(1, (512, 64)), rng_uniform(2, (64, 256))
     with pytest.raises(capi.HipError, match=r"pipeline depths \{3, 2\}, not 5"):
         _run_depth(a, b, "float32", (256, 128, 32, 4, 2), 1, 5, False)
+
+
+# ------------------------------------------------------------------ direct conv tiles
+
+def test_direct_conv_8x14_tile_matches_8x8():
+    # the 8x14-pixel, 1x4-wave direct conv tile (112x64x16, 224 equal blocks
+    # for C4): exact on integer inputs, bit-identical to the 8x8 tile on the
+    # seeded C4 inputs (same per-output MFMA order over taps and channels)
+    x = ref.np_init((8, 56, 56, 64), "float32") % 5
+    w = ref.np_init((3, 3, 64, 64), "float32") % 3 - 1
+    xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    want = ref.relu(ref.conv2d(xp, w)).astype(np.float32)
+    got = run_conv(x, w, pads=(1, 1, 1, 1), tile=(112, 64, 16, 1, 4), relu=True)
+    np.testing.assert_array_equal(got, want)
+    xs, ws = ref.config_inputs("C4")
+    a = run_conv(xs, ws, pads=(1, 1, 1, 1), tile=(112, 64, 16, 1, 4), relu=True)
+    b = run_conv(xs, ws, pads=(1, 1, 1, 1), tile=(64, 64, 16, 2, 2), relu=True)
+    np.testing.assert_array_equal(a, b)
+    xsp = ref.pad(xs, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    assert ref.scaled_error(a, ref.relu(ref.conv2d(xsp, ws)), 576, np.abs(xsp).max(), np.abs(ws).max()) <= TOL_F32
+
+
+@pytest.mark.parametrize("shape", [(2, 23, 30, 128, 64, 3, 3, 0), (1, 9, 15, 64, 128, 1, 1, 1), (3, 16, 40, 64, 64, 3, 3, 2)])
+def test_direct_conv_8x14_ragged(shape):
+    # partial blocks in H and W, more than one channel chunk, 1x1 windows, pads of 0-2
+    n, h, wd, c, f, r, s, pad = shape
+    x = rng_uniform(21, (n, h, wd, c))
+    w = rng_uniform(22, (r, s, c, f))
+    got = run_conv(x, w, pads=(pad, pad, pad, pad), pad_value=0.25, tile=(112, 64, 16, 1, 4))
+    xp = ref.pad(x, [(0, 0), (pad, pad), (pad, pad), (0, 0)], 0.25)
+    assert ref.scaled_error(got, ref.conv2d(xp, w), r * s * c, np.abs(xp).max(), 1.0) <= TOL_F32
+
+
+def test_direct_only_conv_tile_rejects_other_shapes():
+    x, w = rng_uniform(1, (1, 20, 20, 64)), rng_uniform(2, (3, 3, 64, 64))
+    with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
+        run_conv(x, w, stride=(2, 2), tile=(112, 64, 16, 1, 4))

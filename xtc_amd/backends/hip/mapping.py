@@ -119,10 +119,25 @@ def _level(sched: HipNodeSchedule, dims: list[str], level: int) -> int | None:
     return out
 
 
-def _default(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int], int]:
+def _default(dtype: str, conv: bool, M: int, N: int, K: int,
+             attrs: dict[str, Any] | None = None) -> tuple[tuple[int, int, int, int, int], int]:
     from ...runtimes.hip import capi
 
+    if conv and attrs is not None:
+        return default_conv_tile(attrs)
     return capi.default_tile(dtype, conv, M, N, K)
+
+
+def default_conv_tile(attrs: dict[str, Any]) -> tuple[tuple[int, int, int, int, int], int]:
+    """The library's default (tile, split_k) for a conv2d launch: it sees the
+    window and strides (xtc_hip_conv2d_default_tile)."""
+    from ...runtimes.hip import capi
+
+    _, nb, h, w, c, f, r, s, (sh, sw), (pt, pb, pl, pr) = _attrs_key(attrs, True)
+    dt = capi.XTC_HIP_F32 if attrs["dtype"] == "float32" else capi.XTC_HIP_BF16
+    cd = capi.Conv2dDesc(dtype=dt, N=nb, H=h, W=w, C=c, F=f, R=r, S=s, stride_h=sh, stride_w=sw, pad_top=pt,
+                         pad_bottom=pb, pad_left=pl, pad_right=pr)
+    return capi.conv2d_default_tile(cd)
 
 
 def _attrs_key(attrs: dict[str, Any], conv: bool) -> tuple[Any, ...]:
@@ -216,7 +231,7 @@ def map_gemm(
     if not cands:
         raise ScheduleError(f"no compiled {'conv' if conv else 'matmul'} instance for {dtype}")
     if sched is None or not any(sched.levels(d) for d in sched.dims) and not sched.parallelization:
-        tile, split = _default(dtype, conv, M, N, K)
+        tile, split = _default(dtype, conv, M, N, K, launch_attrs)
         return GemmConfig(dtype, conv, *tile, split_k=split, exact=True, source="default")
     if sched.splits:
         raise ScheduleError(f"{sched.node_name}: split() has no HIP kernel mapping")
@@ -241,7 +256,7 @@ def map_gemm(
     col_major = bool(order) and order.index(n_dims[0]) < min(order.index(d) for d in m_dims if d in order)
     group_m = (M + (bm or 64) - 1) // (bm or 64) if col_major else DEFAULT_GROUP_M
 
-    dflt_tile, dflt_split = _default(dtype, conv, M, N, K)
+    dflt_tile, dflt_split = _default(dtype, conv, M, N, K, launch_attrs)
     req_bm = bm or dflt_tile[0]
     req_bn = bn or dflt_tile[1]
     req_bk = bk or dflt_tile[2]
@@ -256,6 +271,21 @@ def map_gemm(
     ]
     _check_vectorize(sched, dtype)
     depth = _requested_depth(sched, k_dims, k_parallel)
+    if conv:
+        # some conv tiles exist only in the direct kernel, for the shapes it takes
+        from ...runtimes.hip import capi
+
+        runnable = []
+        for t in matches:
+            try:
+                pipeline_depths(launch_attrs, conv, t, split_k)
+                runnable.append(t)
+            except capi.HipError:
+                pass
+        if matches and not runnable and policy == "strict":
+            raise ScheduleError(f"{sched.node_name}: conv tile {matches[0]} has no kernel for this shape "
+                                "(it exists only in the direct conv kernel)")
+        matches = runnable
     if matches:
         # unspecified wave split: the instance with the most waves
         tile = max(matches, key=lambda t: (t[3] * t[4], t[3]))

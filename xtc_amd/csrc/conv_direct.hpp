@@ -9,9 +9,10 @@
 // Why not the implicit-GEMM loader: for shapes like 8x56x56x64 * 3x3x64x64
 // (GEMM M=25088, N=64, K=576) each tile walks only K=576 and re-reads every
 // input pixel once per filter tap from L2; the global-load latency is then
-// exposed on every slab.  Here a workgroup owns an 8x8 block of output
-// pixels x 64 filters of one image:
-//   * the input halo ((8-1)*sh+R) x ((8-1)*sw+S) pixels x 64 channels is
+// exposed on every slab.  Here a workgroup owns a TH x TW block of output
+// pixels x 64 filters of one image (8x8 with 2x2 waves, or 8x14 with 1x4
+// waves: 224 equal blocks for 8x56x56 outputs, one per CU):
+//   * the input halo ((TH-1)*sh+R) x ((TW-1)*sw+S) pixels x 64 channels is
 //     loaded once into LDS (pad_value outside the image), pixel stride 68
 //     floats so the 16 pixels read by a lane group fall on distinct banks;
 //   * the weights stream one tap (r, s) [64 c][64 f] = 16 KB at a time
@@ -20,9 +21,9 @@
 //     ahead; the 16-byte chunks of
 //     weight row c are XOR-swizzled by 4*((c>>2)&3) so the scalar B reads of
 //     the four lane groups hit disjoint banks;
-//   * 4 waves (2x2), each 32 pixels x 32 filters of v_mfma_f32_16x16x4_f32;
-//     the filter fragment is the first operand, so a lane ends up with 4
-//     consecutive filters of one pixel and stores a float4;
+//   * 4 waves (WM x WN), each TH*TW/WM pixels x 64/WN filters of
+//     v_mfma_f32_16x16x4_f32; the filter fragment is the first operand, so a
+//     lane ends up with 4 consecutive filters of one pixel and stores a float4;
 //   * more than 64 channels: the halo is reloaded per 64-channel chunk.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -44,7 +45,7 @@ struct DirectConvArgs {
   float pad_value;
   int relu;
   float relu_threshold;
-  int tiles_h, tiles_w;  // ceil(OH/8), ceil(OW/8)
+  int tiles_h, tiles_w;  // ceil(OH/TH), ceil(OW/TW)
 };
 
 namespace dconv {
@@ -53,23 +54,31 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int TH = 8, TW = 8;     // output pixels per workgroup
 constexpr int CB = 64;            // channels per chunk
 constexpr int FB = 64;            // filters per workgroup
 constexpr int CP = CB + 4;        // halo pixel stride (floats)
 constexpr int W_STAGE = CB * FB * 4;  // 16 KB
 constexpr int STAGES = 3;
-constexpr int HALO_MAX_BYTES = 32 * 1024;
-constexpr int HALO_MAX_PIX = HALO_MAX_BYTES / (CP * 4);  // 120 pixels
-constexpr int DMA_PER_WAVE = W_STAGE / 1024 / 4;          // 4
+constexpr int NW = 4;             // waves per workgroup
+constexpr int NT = NW * 64;
+constexpr int DMA_PER_WAVE = W_STAGE / 1024 / NW;  // 4
+// halo capacity in pixels for a halo buffer of `bytes`
+constexpr int halo_pix(int bytes) { return bytes / (CP * 4); }
 
 __device__ __forceinline__ int swz(int c) { return 4 * ((c >> 2) & 3); }
 constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 
 }  // namespace dconv
 
+// TH x TW output pixels per workgroup, WM x WN waves, HALO_BYTES of LDS for
+// the input halo of one 64-channel chunk.
+template <int TH, int TW, int WM, int WN, int HALO_BYTES>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_direct_f32(DirectConvArgs a) {
   using namespace dconv;
+  constexpr int HALO_MAX_PIX = halo_pix(HALO_BYTES);
+  constexpr int PT = TH * TW / 16 / WM;  // 16-pixel tiles per wave
+  constexpr int FT = FB / WN / 16;       // 16-filter tiles per wave
+  static_assert(WM * WN == NW && TH * TW % (16 * WM) == 0 && FB % (16 * WN) == 0, "tiling");
   __shared__ __attribute__((aligned(1024))) float halo[HALO_MAX_PIX * CP];
   __shared__ __attribute__((aligned(1024))) unsigned char w0[W_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char w1[W_STAGE];
@@ -79,8 +88,8 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1;  // pixel half: pixels 32 wm .. +31
-  const int wn = wave & 1;   // filter half: filters 32 wn .. +31
+  const int wm = wave / WN;  // pixels 16 PT wm .. +16 PT - 1
+  const int wn = wave % WN;  // filters 16 FT wn .. +16 FT - 1
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
@@ -120,15 +129,15 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
   };
 
   // All of a thread's halo loads are issued before its first LDS write (at
-  // most HALO_MAX_PIX * 16 / 256 = 8 chunks), so the load latency is paid
-  // once rather than once per chunk.
+  // most HALO_MAX_PIX * 16 / 256 chunks: 8 for 8x8 tiles, 12 for 8x14), so
+  // the load latency is paid once rather than once per chunk.
   auto load_halo = [&](int chunk) {
-    constexpr int MAXQ = (HALO_MAX_PIX * (CB / 4) + 255) / 256;
+    constexpr int MAXQ = (HALO_MAX_PIX * (CB / 4) + NT - 1) / NT;
     const int n16 = HH * HW * (CB / 4);  // 16-byte chunks
     f32x4 v[MAXQ];
 #pragma unroll
     for (int j = 0; j < MAXQ; ++j) {
-      const int q = tid + j * 256;
+      const int q = tid + j * NT;
       const int pix = q >> 4;
       const int cc = (q & 15) * 4;
       const int hy = pix / HW, hx = pix - (pix / HW) * HW;
@@ -139,25 +148,25 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     }
 #pragma unroll
     for (int j = 0; j < MAXQ; ++j) {
-      const int q = tid + j * 256;
+      const int q = tid + j * NT;
       if (q < n16) *(f32x4*)(halo + (q >> 4) * CP + (q & 15) * 4) = v[j];
     }
   };
 
-  // output pixels of this lane's two 16-pixel tiles
-  int php[2], pwp[2];
+  // output pixels of this lane's PT 16-pixel tiles
+  int php[PT], pwp[PT];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int p = wm * 32 + it * 16 + l16;
+  for (int it = 0; it < PT; ++it) {
+    const int p = wm * 16 * PT + it * 16 + l16;
     php[it] = p / TW;
     pwp[it] = p % TW;
   }
 
-  f32x4 acc[2][2];
+  f32x4 acc[PT][FT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < PT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int t = 0; t < STAGES - 1; ++t)
@@ -179,23 +188,23 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     const float* ws = (const float*)wst[s];
     const int r = tap / a.S;
     const int sx = tap - r * a.S;
-    int aoff[2];
+    int aoff[PT];
 #pragma unroll
-    for (int it = 0; it < 2; ++it) aoff[it] = ((php[it] * a.sh + r) * HW + pwp[it] * a.sw + sx) * CP + 4 * g;
+    for (int it = 0; it < PT; ++it) aoff[it] = ((php[it] * a.sh + r) * HW + pwp[it] * a.sw + sx) * CP + 4 * g;
 #pragma unroll
     for (int kc = 0; kc < CB / 16; ++kc) {
-      f32x4 av[2];
+      f32x4 av[PT];
 #pragma unroll
-      for (int it = 0; it < 2; ++it) av[it] = *(const f32x4*)(halo + aoff[it] + kc * 16);
+      for (int it = 0; it < PT; ++it) av[it] = *(const f32x4*)(halo + aoff[it] + kc * 16);
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int c = kc * 16 + 4 * g + st;
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) {
-          const int f = wn * 32 + jt * 16 + l16;
+        for (int jt = 0; jt < FT; ++jt) {
+          const int f = wn * 16 * FT + jt * 16 + l16;
           const float bv = ws[c * FB + ((f >> 2) ^ swz(c)) * 4 + (f & 3)];
 #pragma unroll
-          for (int it = 0; it < 2; ++it)
+          for (int it = 0; it < PT; ++it)
             acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av[it][st], acc[it][jt], 0, 0, 0);
         }
       }
@@ -209,13 +218,13 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
 
   // lane holds filters f0 .. f0+3 of pixel (php, pwp) for each (it, jt)
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
+  for (int it = 0; it < PT; ++it) {
     const int oh = oh0 + php[it], ow = ow0 + pwp[it];
     if (oh >= a.OH || ow >= a.OW) continue;
     float* out = a.O + (((size_t)img * a.OH + oh) * a.OW + ow) * a.F + fb * FB;
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      const int f = wn * 32 + jt * 16 + 4 * g;
+    for (int jt = 0; jt < FT; ++jt) {
+      const int f = wn * 16 * FT + jt * 16 + 4 * g;
       f32x4 v = acc[it][jt];
       if (a.bias) v += *(const f32x4*)(a.bias + fb * FB + f);
       if (a.relu) {

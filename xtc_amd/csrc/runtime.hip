@@ -400,6 +400,59 @@ int grid_for(uint64_t n, int block) {
   return (int)g;
 }
 
+// Tiles of the direct conv kernel (conv_direct.hpp): BM output pixels as a
+// TH x TW block, 64 filters, slabs of 16 channels per MFMA k-group, WGM x WGN
+// waves, and the LDS of the input halo.  8x8 (2x2 waves) shares its tile
+// with a generic implicit-GEMM instance, which runs the shapes the direct
+// kernel does not take; 8x14 (1x4 waves, 224 equal blocks for 8x56x56
+// outputs: one per CU) exists only here.
+typedef void (*DirectConvLaunch)(const DirectConvArgs&, dim3, hipStream_t);
+template <int TH, int TW, int WM, int WN, int HALO_BYTES>
+void launch_conv_direct(const DirectConvArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((conv_direct_f32<TH, TW, WM, WN, HALO_BYTES>), grid, dim3(dconv::NT), 0, s, a);
+}
+struct DirectConvTile {
+  xtc_hip_tile tile;
+  int th, tw, halo_bytes;
+  DirectConvLaunch launch;
+};
+const DirectConvTile kDirectConv[] = {
+    {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, &launch_conv_direct<8, 8, 2, 2, 32 * 1024>},
+    {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, &launch_conv_direct<8, 14, 1, 4, 48 * 1024>},
+};
+
+bool same_tile(const xtc_hip_tile& a, const xtc_hip_tile& b) {
+  return a.bm == b.bm && a.bn == b.bn && a.bk == b.bk && a.wgm == b.wgm && a.wgn == b.wgn;
+}
+
+const DirectConvTile* direct_conv_tile(const xtc_hip_tile& t) {
+  for (const DirectConvTile& d : kDirectConv)
+    if (same_tile(d.tile, t)) return &d;
+  return nullptr;
+}
+
+// Registry entries of the tiles only the direct conv kernel implements
+// (launch null: no implicit-GEMM instance behind them).
+const GemmEntry* direct_only_entries(int* n) {
+  static const std::vector<GemmEntry> v = [] {
+    std::vector<GemmEntry> out;
+    int nreg = 0;
+    const GemmEntry* e = gemm_registry(&nreg);
+    for (const DirectConvTile& d : kDirectConv) {
+      bool generic = false;
+      for (int i = 0; i < nreg; ++i)
+        generic = generic || (e[i].dtype == XTC_HIP_F32 && e[i].conv == 1 &&
+                              same_tile(xtc_hip_tile{e[i].bm, e[i].bn, e[i].bk, e[i].wgm, e[i].wgn}, d.tile));
+      if (!generic)
+        out.push_back(GemmEntry{XTC_HIP_F32, 1, d.tile.bm, d.tile.bn, d.tile.bk, d.tile.wgm, d.tile.wgn,
+                                d.halo_bytes + dconv::STAGES * dconv::W_STAGE, dconv::NT, nullptr});
+    }
+    return out;
+  }();
+  *n = (int)v.size();
+  return v.data();
+}
+
 const GemmEntry* find_entry(int dtype, int conv, const xtc_hip_tile& t) {
   int n = 0;
   const GemmEntry* e = gemm_registry(&n);
@@ -408,6 +461,10 @@ const GemmEntry* find_entry(int dtype, int conv, const xtc_hip_tile& t) {
         e[i].bk == t.bk && e[i].wgm == t.wgm && e[i].wgn == t.wgn)
       return &e[i];
   }
+  const GemmEntry* x = direct_only_entries(&n);
+  for (int i = 0; i < n; ++i)
+    if (x[i].dtype == dtype && x[i].conv == conv && same_tile(xtc_hip_tile{x[i].bm, x[i].bn, x[i].bk, x[i].wgm, x[i].wgn}, t))
+      return &x[i];
   return nullptr;
 }
 
@@ -729,27 +786,31 @@ int launch_skinny_gemm(const xtc_hip_matmul_desc& d, int split_k, int stages, in
   return 0;
 }
 
-// The direct conv kernel (conv_direct.hpp) implements the conv tile 64x64x16
-// with 2x2 waves for fp32 when C and F are multiples of 64 and the input
-// halo of an 8x8 output block fits its LDS buffer.
+// The direct conv kernel (conv_direct.hpp) implements the tiles of
+// kDirectConv for fp32 when C and F are multiples of 64 and the input halo
+// of one output block fits its LDS buffer.  XTC_HIP_GENERIC_GEMM=1 turns it
+// off for the tiles a generic instance also implements.
 bool direct_conv_applies(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int split_k, int OH, int OW,
                          const void* I, const void* W, const void* O, const void* bias) {
   static const bool disabled = [] {
     const char* v = getenv("XTC_HIP_GENERIC_GEMM");
     return v && v[0] == '1';
   }();
-  if (disabled || d.dtype != XTC_HIP_F32 || split_k > 1) return false;
-  if (t.bm != 64 || t.bn != 64 || t.bk != 16 || t.wgm != 2 || t.wgn != 2) return false;
+  const DirectConvTile* dt = direct_conv_tile(t);
+  const GemmEntry* e = find_entry(XTC_HIP_F32, 1, t);
+  const bool direct_only = e && e->launch == nullptr;
+  if (!dt || (disabled && !direct_only) || d.dtype != XTC_HIP_F32 || split_k > 1) return false;
   if (d.C % 64 || d.F % 64) return false;
-  const int hh = 7 * d.stride_h + d.R, hw = 7 * d.stride_w + d.S;
-  if (hh * hw > dconv::HALO_MAX_PIX) return false;
+  const int hh = (dt->th - 1) * d.stride_h + d.R, hw = (dt->tw - 1) * d.stride_w + d.S;
+  if (hh * hw > dconv::halo_pix(dt->halo_bytes)) return false;
   if (!aligned16(I) || !aligned16(W) || !aligned16(O) || (bias && !aligned16(bias))) return false;
   if ((int64_t)d.R * d.S * d.C * d.F > INT32_MAX || (int64_t)d.N * OH * OW > INT32_MAX) return false;
   return true;
 }
 
-int launch_direct_conv(const xtc_hip_conv2d_desc& d, int OH, int OW, const void* I, const void* W, float* O,
-                       const float* bias, hipStream_t s) {
+int launch_direct_conv(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int OH, int OW, const void* I,
+                       const void* W, float* O, const float* bias, hipStream_t s) {
+  const DirectConvTile* dt = direct_conv_tile(t);
   DirectConvArgs a;
   a.I = (const float*)I;
   a.Wt = (const float*)W;
@@ -771,13 +832,25 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, int OH, int OW, const void*
   a.pad_value = d.pad_value;
   a.relu = d.relu;
   a.relu_threshold = d.relu_threshold;
-  a.tiles_h = (OH + dconv::TH - 1) / dconv::TH;
-  a.tiles_w = (OW + dconv::TW - 1) / dconv::TW;
+  a.tiles_h = (OH + dt->th - 1) / dt->th;
+  a.tiles_w = (OW + dt->tw - 1) / dt->tw;
   const uint64_t blocks = (uint64_t)d.N * a.tiles_h * a.tiles_w * (d.F / dconv::FB);
   if (blocks > 0x7fffffffu) return fail("conv2d grid too large");
-  hipLaunchKernelGGL(conv_direct_f32, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  dt->launch(a, dim3((unsigned)blocks), s);
   HIP_TRY(hipGetLastError());
   return 0;
+}
+
+// The tile a conv2d descriptor gets when it leaves `tile` zeroed: the shape
+// class default of default_tile, upgraded from the 8x8 direct conv block to
+// the 8x14 one (one block per CU for 8x56x56 outputs; 6 % faster on C4 in one
+// process) when the direct kernel takes the shape with it.
+void default_conv_tile(const xtc_hip_conv2d_desc& d, int OH, int OW, xtc_hip_tile* t, int* split_k) {
+  default_tile(d.dtype, 1, d.N * OH * OW, d.F, d.R * d.S * d.C, t, split_k);
+  const xtc_hip_tile wide{112, 64, 16, 1, 4};
+  const void* p = (const void*)(uintptr_t)256;
+  if (same_tile(*t, xtc_hip_tile{64, 64, 16, 2, 2}) && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr))
+    *t = wide;
 }
 
 int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int stages, int lda, int ldb,
@@ -1296,15 +1369,21 @@ int xtc_hip_event_destroy(void* event) {
 }
 
 int xtc_hip_gemm_instance_count(void) {
-  int n = 0;
+  int n = 0, m = 0;
   gemm_registry(&n);
-  return n;
+  direct_only_entries(&m);
+  return n + m;
 }
 
 int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance* out) {
-  int n = 0;
+  int n = 0, m = 0;
   const GemmEntry* e = gemm_registry(&n);
-  if (index < 0 || index >= n || !out) return fail("instance index %d out of range", index);
+  const GemmEntry* x = direct_only_entries(&m);
+  if (index < 0 || index >= n + m || !out) return fail("instance index %d out of range", index);
+  if (index >= n) {
+    e = x;
+    index -= n;
+  }
   out->dtype = e[index].dtype;
   out->conv = e[index].conv;
   out->tile = xtc_hip_tile{e[index].bm, e[index].bn, e[index].bk, e[index].wgm, e[index].wgn};
@@ -1318,6 +1397,17 @@ int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile*
   if (!out || !split_k) return fail("null output");
   default_tile(dtype, conv, M, N, K, out, split_k);
   if (out->bm == 0) return fail("no kernel instance for dtype %d conv %d", dtype, conv);
+  return 0;
+}
+
+int xtc_hip_conv2d_default_tile(const xtc_hip_conv2d_desc* desc, xtc_hip_tile* out, int* split_k) {
+  if (!desc || !out || !split_k) return fail("null argument");
+  const xtc_hip_conv2d_desc& d = *desc;
+  const int HP = d.H + d.pad_top + d.pad_bottom;
+  const int WP = d.W + d.pad_left + d.pad_right;
+  if (d.stride_h <= 0 || d.stride_w <= 0 || HP < d.R || WP < d.S) return fail("bad conv2d descriptor");
+  default_conv_tile(d, (HP - d.R) / d.stride_h + 1, (WP - d.S) / d.stride_w + 1, out, split_k);
+  if (out->bm == 0) return fail("no conv2d kernel instance for dtype %d", d.dtype);
   return 0;
 }
 
@@ -1355,11 +1445,22 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
   }
   xtc_hip_tile t = d.tile;
   int split_k = d.split_k;
-  if (t.bm == 0) default_tile(d.dtype, 1, d.N * OH * OW, d.F, d.R * d.S * d.C, &t, &split_k);
+  if (t.bm == 0) default_conv_tile(d, OH, OW, &t, &split_k);
+  const GemmEntry* e = find_entry(d.dtype, 1, t);
+  if (!e)
+    return -fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype, t.bm, t.bn, t.bk,
+                 t.wgm, t.wgn);
   const void* p = (const void*)(uintptr_t)256;
   // the direct kernel streams the weight taps through dconv::STAGES stages;
   // the implicit-GEMM loader double-buffers through registers
-  depths[0] = direct_conv_applies(d, t, split_k, OH, OW, p, p, p, nullptr) ? dconv::STAGES : 2;
+  if (direct_conv_applies(d, t, split_k, OH, OW, p, p, p, nullptr))
+    depths[0] = dconv::STAGES;
+  else if (e->launch)
+    depths[0] = 2;
+  else
+    return -fail("conv2d tile %dx%dx%d waves %dx%d exists only in the direct conv kernel, which does not take "
+                 "this shape",
+                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
   return 1;
 }
 
@@ -1423,7 +1524,7 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   int split_k = d.split_k;
   if (t.bm == 0) {
     int sk = 1;
-    default_tile(d.dtype, 1, M, d.F, K, &t, &sk);
+    default_conv_tile(d, OH, OW, &t, &sk);
     if (split_k <= 0) split_k = sk;
   }
   const GemmEntry* e = find_entry(d.dtype, 1, t);
@@ -1431,7 +1532,12 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
     return fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
   if (direct_conv_applies(d, t, split_k, OH, OW, input, weight, out, bias))
-    return launch_direct_conv(d, OH, OW, input, weight, out, bias, s);
+    return launch_direct_conv(d, t, OH, OW, input, weight, out, bias, s);
+  if (!e->launch)
+    return fail("conv2d tile %dx%dx%d waves %dx%d exists only in the direct conv kernel, which needs fp32, no "
+                "split-K, C and F multiples of 64, 16-byte aligned operands and an input halo that fits its "
+                "LDS buffer",
+                t.bm, t.bn, t.bk, t.wgm, t.wgn);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A = input;

@@ -164,6 +164,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _i,
         [_i, _i, _i, _i, _i, ctypes.POINTER(Tile), ctypes.POINTER(_i)],
     ),
+    "xtc_hip_conv2d_default_tile": (_i, [ctypes.POINTER(Conv2dDesc), ctypes.POINTER(Tile), ctypes.POINTER(_i)]),
     "xtc_hip_matmul_pipeline_depths": (_i, [ctypes.POINTER(MatmulDesc), ctypes.POINTER(_i), _i]),
     "xtc_hip_conv2d_pipeline_depths": (_i, [ctypes.POINTER(Conv2dDesc), ctypes.POINTER(_i), _i]),
     "xtc_hip_evaluate_perf": (
@@ -277,3 +278,11 @@ def conv2d_pipeline_depths(desc: Conv2dDesc) -> list[int]:
     if n < 0:
         raise HipError(f"conv2d_pipeline_depths: {last_error()}")
     return list(out[: min(n, 16)])
+
+
+def conv2d_default_tile(desc: Conv2dDesc) -> tuple[tuple[int, int, int, int, int], int]:
+    """(tile, split_k) a conv2d descriptor gets when it leaves the tile zeroed."""
+    t = Tile()
+    sk = ctypes.c_int(1)
+    check(lib().xtc_hip_conv2d_default_tile(ctypes.byref(desc), ctypes.byref(t), ctypes.byref(sk)), "conv2d_default_tile")
+    return t.as_tuple(), int(sk.value)

@@ -620,13 +620,19 @@ class Strategy_HIP(BaseStrategy):
         return pipeline_depths(self._attrs, self._conv, tile, split)
 
     def _points(self) -> list[list[int]]:
+        from ..runtimes.hip import capi
+
         out = []
         for tile in self._tiles:
             bm, bn, bk, wgm, wgn = tile
             for s in self._splits:
                 if s > 1 and (self._K // s) % bk:
                     continue
-                for depth in self._depths(tile, s):
+                try:
+                    depths = self._depths(tile, s)
+                except capi.HipError:  # a tile with no kernel for this shape
+                    continue
+                for depth in depths:
                     out.append([bm, bm // wgm, bn, bn // wgn, bk, s, depth])
         return out
 
@@ -673,7 +679,12 @@ class Strategy_HIP(BaseStrategy):
     def _default_schedule(self, opt_level: int) -> list[int]:
         from ..runtimes.hip import capi
 
-        tile, split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
+        if self._conv:
+            from ..backends.hip.mapping import default_conv_tile
+
+            tile, split = default_conv_tile(self._attrs)
+        else:
+            tile, split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
         bm, bn, bk, wgm, wgn = tile
         split = max(1, split)
         return [bm, bm // wgm, bn, bn // wgn, bk, split, self._depths(tile, split)[0]]
