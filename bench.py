@@ -146,6 +146,65 @@ def _print_peaks() -> int:
     return 0
 
 
+def _elementwise(steps: int) -> int:
+    """HBM rate of the elementwise kernels, one JSON line each: relu, pad,
+    the bf16 casts (library entry points) and the transpose that stages a
+    transposed matmul operand (timed inside a trans_a matmul with N = 16, so
+    its rate is read from the kernel trace: the line's time includes the
+    skinny GEMM).  Bytes are algorithmic: every input element read once, every
+    output element written once."""
+    import numpy as np
+
+    from xtc_amd.runtimes.hip import capi
+    from xtc_amd.runtimes.hip.buffer import DeviceBuffer, ensure_device
+
+    ensure_device(0)
+    L = capi.lib()
+    e0, e1 = L.xtc_hip_event_create(), L.xtc_hip_event_create()
+
+    def timed(name: str, nbytes: int, launch) -> None:  # type: ignore[no-untyped-def]
+        for _ in range(3):
+            launch()
+        capi.check(L.xtc_hip_event_record(e0, None), "event")
+        for _ in range(steps):
+            launch()
+        capi.check(L.xtc_hip_event_record(e1, None), "event")
+        ms = ctypes.c_float()
+        capi.check(L.xtc_hip_event_elapsed_ms(e0, e1, ctypes.byref(ms)), "elapsed")
+        us = ms.value * 1e3 / steps
+        print(json.dumps({"kernel": name, "bytes": nbytes, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                          "frac_of_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}), flush=True)
+
+    n = 1 << 26  # 256 MiB of fp32
+    x = DeviceBuffer(n * 4)
+    y = DeviceBuffer(n * 4)
+    h = DeviceBuffer(n * 2)
+    x.zero()
+    h.zero()
+    xp, yp, hp = ctypes.c_void_p(x.ptr), ctypes.c_void_p(y.ptr), ctypes.c_void_p(h.ptr)
+    timed("relu_kernel fp32 2^26", 8 * n, lambda: capi.check(L.xtc_hip_relu(xp, yp, n, 0.0, None), "relu"))
+    timed("cast_f32_bf16_kernel 2^26", 6 * n, lambda: capi.check(L.xtc_hip_cast_f32_to_bf16(xp, hp, n, None), "cast"))
+    timed("cast_bf16_f32_kernel 2^26", 6 * n, lambda: capi.check(L.xtc_hip_cast_bf16_to_f32(hp, yp, n, None), "cast"))
+    for shape, pads in (((64, 112, 112, 64), ((0, 0), (1, 1), (1, 1), (0, 0))),
+                        ((8, 56, 56, 64), ((0, 0), (0, 0), (0, 0), (1, 3)))):
+        nd = len(shape)
+        sh = (ctypes.c_int64 * nd)(*shape)
+        be = (ctypes.c_int64 * nd)(*[p[0] for p in pads])
+        af = (ctypes.c_int64 * nd)(*[p[1] for p in pads])
+        out_elems = int(np.prod([d + p[0] + p[1] for d, p in zip(shape, pads)]))
+        nbytes = 4 * (int(np.prod(shape)) + out_elems)
+        timed(f"pad_kernel {'x'.join(map(str, shape))} pads {[list(p) for p in pads]}", nbytes,
+              lambda sh=sh, be=be, af=af: capi.check(L.xtc_hip_pad(xp, yp, nd, sh, be, af, 0.0, None), "pad"))
+    # transposed A: the library stages A^T [K][M] into A [M][K] with transpose_kernel
+    for dtype, esz in (("float32", 4), ("bfloat16", 2)):
+        d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, M=8192, N=16,
+                            K=8192, trans_a=1, xcd_remap=1)
+        timed(f"matmul trans_a {dtype} 8192x16x8192 (transpose_kernel + skinny GEMM)", 2 * esz * 8192 * 8192,
+              lambda d=d: capi.check(L.xtc_hip_matmul(ctypes.byref(d), xp, yp, hp, None), "matmul"))
+    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    return 0
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -186,6 +245,8 @@ def main(argv: list[str] | None = None) -> int:
                     help="skip the evaluate_perf protocol pass (kernel traces then hold only the timed steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the measured MFMA ceiling")
+    ap.add_argument("--elementwise", action="store_true",
+                    help="only time the elementwise kernels (relu, pad, bf16 casts, transpose) in GB/s")
     ap.add_argument("--peak", action="store_true",
                     help="only print the measured MFMA peaks (fp32, bf16; zero, random and the reference's operands)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
@@ -197,6 +258,8 @@ def main(argv: list[str] | None = None) -> int:
         return _calibrate_copy(args.steps)
     if args.peak:
         return _print_peaks()
+    if args.elementwise:
+        return _elementwise(args.steps)
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU; a GEMM "

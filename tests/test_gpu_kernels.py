@@ -337,6 +337,51 @@ def test_pad_kernel():
     np.testing.assert_array_equal(Y.to_numpy(expect.shape, np.float32), expect)
 
 
+@pytest.mark.parametrize("shape,pads", [
+    ((2, 9, 11, 64), [(0, 0), (1, 1), (2, 0), (0, 0)]),   # 16-byte row copies (innermost dim unpadded)
+    ((4, 8), [(3, 2), (0, 0)]),
+    ((12,), [(0, 0)]),                                      # rank 1, no padding: a copy
+    ((2, 9, 11, 6), [(0, 0), (1, 1), (1, 1), (0, 0)]),    # rows of 6 floats: element path
+])
+def test_pad_kernel_paths(shape, pads):
+    x = rng_uniform(13, shape)
+    nd = len(shape)
+    X = DeviceBuffer.from_numpy(x)
+    expect = ref.pad(x, pads, 0.5)
+    Y = DeviceBuffer(expect.nbytes)
+    L = capi.lib()
+    capi.check(L.xtc_hip_pad(X.c_ptr, Y.c_ptr, nd, (ctypes.c_int64 * nd)(*shape),
+                             (ctypes.c_int64 * nd)(*[p[0] for p in pads]), (ctypes.c_int64 * nd)(*[p[1] for p in pads]),
+                             ctypes.c_float(0.5), None))
+    capi.check(L.xtc_hip_synchronize())
+    np.testing.assert_array_equal(Y.to_numpy(expect.shape, np.float32), expect)
+
+
+@pytest.mark.parametrize("offset", [0, 2])
+def test_cast_bf16_vector_and_unaligned(offset):
+    # offset 0: 16-byte aligned, 8 elements per thread step plus a tail of 5;
+    # offset 2 elements: unaligned pointers, one element at a time
+    n = 8 * 1000 + 5
+    x = rng_uniform(14, (n + offset,), -3, 3)
+    x[offset:offset + 4] = [np.nan, np.inf, -0.0, 1e-40]
+    X = DeviceBuffer.from_numpy(x)
+    H = DeviceBuffer((n + offset) * 2)
+    Y = DeviceBuffer((n + offset) * 4)
+    L = capi.lib()
+    capi.check(L.xtc_hip_cast_f32_to_bf16(ctypes.c_void_p(X.ptr + 4 * offset), ctypes.c_void_p(H.ptr + 2 * offset), n,
+                                          None))
+    capi.check(L.xtc_hip_cast_bf16_to_f32(ctypes.c_void_p(H.ptr + 2 * offset), ctypes.c_void_p(Y.ptr + 4 * offset), n,
+                                          None))
+    capi.check(L.xtc_hip_synchronize())
+    bits = H.to_numpy((n + offset,), np.uint16)[offset:]
+    want = f32_to_bf16_bits(x[offset:])
+    nan = np.isnan(x[offset:])
+    np.testing.assert_array_equal(bits[~nan], want[~nan])
+    assert np.all((bits[nan] & 0x7F80) == 0x7F80) and np.all(bits[nan] & 0x7F)
+    back = Y.to_numpy((n + offset,), np.float32)[offset:]
+    np.testing.assert_array_equal(back[~nan], ref.round_bf16(x[offset:])[~nan])
+
+
 def test_cast_bf16_roundtrip():
     x = rng_uniform(12, (4099,), -100, 100)
     x[:4] = [np.inf, -np.inf, 0.0, -0.0]

@@ -305,6 +305,32 @@ __global__ void pad_kernel(const float* __restrict__ x, float* __restrict__ y, P
   }
 }
 
+// Constant pad with no padding on the innermost dim: the output is rows of
+// that dim, each a copy of one input row or all `value`; 16-byte accesses
+// (the row length and both pointers are multiples of 4 floats / 16 bytes).
+// The row index is decomposed over the outer dims once per 4 elements.
+__global__ void pad_rows_kernel(const float4* __restrict__ x, float4* __restrict__ y, PadDims d, uint64_t total4,
+                                float value) {
+  const int inner4 = (int)(d.out_shape[d.ndim - 1] / 4);
+  const float4 pv = make_float4(value, value, value, value);
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total4; i += stride) {
+    uint64_t row = i / (uint64_t)inner4;
+    const int col = (int)(i - row * (uint64_t)inner4);
+    int64_t src = 0, src_stride = 1;
+    bool inside = true;
+    for (int k = d.ndim - 2; k >= 0; --k) {
+      const int64_t o = (int64_t)(row % (uint64_t)d.out_shape[k]);
+      row /= (uint64_t)d.out_shape[k];
+      const int64_t sk = o - d.before[k];
+      inside = inside && sk >= 0 && sk < d.in_shape[k];
+      src += sk * src_stride;
+      src_stride *= d.in_shape[k];
+    }
+    y[i] = inside ? x[src * inner4 + col] : pv;
+  }
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   unsigned u = __float_as_uint(f);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
@@ -312,16 +338,49 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)((u + r) >> 16);
 }
 
-__global__ void cast_f32_bf16_kernel(const float* x, uint16_t* y, uint64_t n) {
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) y[i] = f32_to_bf16_rne(x[i]);
+// The casts move 8 elements per thread and step (two 16-byte fp32 accesses,
+// one 16-byte bf16 access) when both pointers are 16-byte aligned; the last
+// n % 8 elements, or all of them otherwise, one at a time.
+__global__ void cast_f32_bf16_kernel(const float* x, uint16_t* y, uint64_t n, int vec) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint64_t done = 0;
+  if (vec) {
+    const uint64_t n8 = n / 8;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    uint4* y8 = reinterpret_cast<uint4*>(y);
+    for (uint64_t i = tid; i < n8; i += stride) {
+      const float4 a = x4[2 * i], b = x4[2 * i + 1];
+      uint4 o;
+      o.x = f32_to_bf16_rne(a.x) | ((unsigned)f32_to_bf16_rne(a.y) << 16);
+      o.y = f32_to_bf16_rne(a.z) | ((unsigned)f32_to_bf16_rne(a.w) << 16);
+      o.z = f32_to_bf16_rne(b.x) | ((unsigned)f32_to_bf16_rne(b.y) << 16);
+      o.w = f32_to_bf16_rne(b.z) | ((unsigned)f32_to_bf16_rne(b.w) << 16);
+      y8[i] = o;
+    }
+    done = n8 * 8;
+  }
+  for (uint64_t i = done + tid; i < n; i += stride) y[i] = f32_to_bf16_rne(x[i]);
 }
 
-__global__ void cast_bf16_f32_kernel(const uint16_t* x, float* y, uint64_t n) {
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) y[i] = __uint_as_float(((unsigned)x[i]) << 16);
+__global__ void cast_bf16_f32_kernel(const uint16_t* x, float* y, uint64_t n, int vec) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint64_t done = 0;
+  if (vec) {
+    const uint64_t n8 = n / 8;
+    const uint4* x8 = reinterpret_cast<const uint4*>(x);
+    float4* y4 = reinterpret_cast<float4*>(y);
+    for (uint64_t i = tid; i < n8; i += stride) {
+      const uint4 v = x8[i];
+      y4[2 * i] = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                              __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+      y4[2 * i + 1] = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                                  __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u));
+    }
+    done = n8 * 8;
+  }
+  for (uint64_t i = done + tid; i < n; i += stride) y[i] = __uint_as_float(((unsigned)x[i]) << 16);
 }
 
 template <typename T>
@@ -1595,6 +1654,13 @@ int xtc_hip_pad(const float* x, float* y, int ndim, const int64_t* shape, const 
     total *= (uint64_t)d.out_shape[k];
   }
   if (total == 0) return 0;
+  const int last = ndim - 1;
+  if (before[last] == 0 && after[last] == 0 && shape[last] % 4 == 0 && aligned16(x) && aligned16(y)) {
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(grid_for(total / 4, 256)), dim3(256), 0, pick_stream(stream),
+                       (const float4*)x, (float4*)y, d, total / 4, value);
+    HIP_TRY(hipGetLastError());
+    return 0;
+  }
   hipLaunchKernelGGL(pad_kernel, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
                      x, y, d, total, value);
   HIP_TRY(hipGetLastError());
@@ -1604,8 +1670,9 @@ int xtc_hip_pad(const float* x, float* y, int ndim, const int64_t* shape, const 
 int xtc_hip_cast_f32_to_bf16(const float* x, uint16_t* y, uint64_t n, void* stream) {
   if (!current_state()) return fail("xtc_hip_init not called");
   if (n == 0) return 0;
-  hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
-                     pick_stream(stream), x, y, n);
+  const int vec = aligned16(x) && aligned16(y);
+  hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3(grid_for(vec ? (n + 7) / 8 : n, 256)), dim3(256), 0,
+                     pick_stream(stream), x, y, n, vec);
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -1613,8 +1680,9 @@ int xtc_hip_cast_f32_to_bf16(const float* x, uint16_t* y, uint64_t n, void* stre
 int xtc_hip_cast_bf16_to_f32(const uint16_t* x, float* y, uint64_t n, void* stream) {
   if (!current_state()) return fail("xtc_hip_init not called");
   if (n == 0) return 0;
-  hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
-                     pick_stream(stream), x, y, n);
+  const int vec = aligned16(x) && aligned16(y);
+  hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(grid_for(vec ? (n + 7) / 8 : n, 256)), dim3(256), 0,
+                     pick_stream(stream), x, y, n, vec);
   HIP_TRY(hipGetLastError());
   return 0;
 }
