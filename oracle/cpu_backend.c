@@ -35,9 +35,10 @@
 #define MIN(a, b) ((a) < (b) ? (a) : (b))
 
 /* C[M,N] = A[M,K] @ B[K,N], fp32, row-major.  One variant per (TI, TK, TJ). */
-#define DEFINE_MATMUL(TI, TK, TJ)                                                        \
-  static void matmul_##TI##_##TK##_##TJ(const float *restrict A, const float *restrict B, \
-                                        float *restrict C, int M, int N, int K) {        \
+#define DEFINE_MATMUL(TI, TK, TJ) DEFINE_MATMUL_FN(matmul_##TI##_##TK##_##TJ, TI, TK, TJ)
+#define DEFINE_MATMUL_FN(NAME, TI, TK, TJ)                                               \
+  static void NAME(const float *restrict A, const float *restrict B,                     \
+                   float *restrict C, int M, int N, int K) {                             \
     _Pragma("omp parallel for schedule(static)") for (int i0 = 0; i0 < M; i0 += TI) {    \
       const int ie = MIN(i0 + TI, M);                                                    \
       for (int i = i0; i < ie; ++i) memset(C + (int64_t)i * N, 0, sizeof(float) * N);    \
@@ -58,6 +59,35 @@
     }                                                                                    \
   }
 
+#if defined(XTC_CPU_TI) && defined(XTC_CPU_TK) && defined(XTC_CPU_TJ)
+/* One sampled schedule, built alone with its tile sizes as compile-time
+ * constants (-DXTC_CPU_TI=.. -DXTC_CPU_TK=.. -DXTC_CPU_TJ=..), as the code
+ * MLIR emits for one loop-explore sample: i1 = TI, k1 = TK, j1 = TJ of the
+ * tile_oo order i, k, j, i1, k1, j1 (oracle/cpu_baseline.py builds one per
+ * sample). */
+DEFINE_MATMUL_FN(matmul_sched, XTC_CPU_TI, XTC_CPU_TK, XTC_CPU_TJ)
+
+static int g_sched_m, g_sched_n, g_sched_k;
+
+void xtc_cpu_sched_configure(int M, int N, int K) {
+  g_sched_m = M;
+  g_sched_n = N;
+  g_sched_k = K;
+}
+
+/* The scheduled matmul called like an XTC module: void f(A, B, C). */
+void xtc_cpu_sched_payload(void *A, void *B, void *C) {
+  matmul_sched((const float *)A, (const float *)B, (float *)C, g_sched_m, g_sched_n, g_sched_k);
+}
+
+int xtc_cpu_sched_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+#else
 DEFINE_MATMUL(4, 64, 64)
 DEFINE_MATMUL(4, 128, 128)
 DEFINE_MATMUL(4, 256, 256)
@@ -162,3 +192,4 @@ int xtc_cpu_configure_matmul(int v, int M, int N, int K) {
 void xtc_cpu_matmul_payload(void *A, void *B, void *C) {
   g_variants[g_cfg_variant].fn((const float *)A, (const float *)B, (float *)C, g_cfg_m, g_cfg_n, g_cfg_k);
 }
+#endif /* single-schedule build */

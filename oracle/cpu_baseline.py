@@ -29,6 +29,9 @@ SRC = HERE / "cpu_backend.c"
 
 __all__ = [
     "load",
+    "schedule_lib",
+    "time_schedule",
+    "autoschedule_tile_oo",
     "threads",
     "matmul",
     "conv2d",
@@ -202,6 +205,87 @@ def time_matmul(a: np.ndarray, b: np.ndarray, variant: int, repeat: int = 3, min
         return float(min(results))
     pa, pb, pc = _fp(a), _fp(b), _fp(c)
     return time_call(lambda: lib.xtc_cpu_matmul(variant, pa, pb, pc, m, n, k), repeat, min_repeat_ms)
+
+
+_sched_libs: dict[tuple[int, int, int], ctypes.CDLL] = {}
+
+
+def schedule_lib(ti: int, tk: int, tj: int) -> ctypes.CDLL:
+    """The restatement built for one tile_oo schedule (i1, k1, j1) =
+    (ti, tk, tj), tiles as compile-time constants; cached per host."""
+    key = (ti, tk, tj)
+    if key in _sched_libs:
+        return _sched_libs[key]
+    out_dir = HERE / "_build" / _host_key()
+    lib = out_dir / f"libxtc_cpu_sched_{ti}_{tk}_{tj}.so"
+    if not lib.exists():
+        out_dir.mkdir(parents=True, exist_ok=True)
+        cc = os.environ.get("CC", "gcc")
+        tmp = lib.with_suffix(f".so.tmp{os.getpid()}")
+        cmd = [cc, "-O3", "-march=native", "-ffp-contract=fast", "-fopenmp", "-fPIC", "-std=c11", "-shared",
+               f"-DXTC_CPU_TI={ti}", f"-DXTC_CPU_TK={tk}", f"-DXTC_CPU_TJ={tj}", "-o", str(tmp), str(SRC)]
+        subprocess.run(cmd, check=True, capture_output=True)
+        os.replace(tmp, lib)
+    handle = ctypes.CDLL(str(lib))
+    handle.xtc_cpu_sched_configure.argtypes = [ctypes.c_int] * 3
+    handle.xtc_cpu_sched_configure.restype = None
+    _sched_libs[key] = handle
+    return handle
+
+
+def time_schedule(tiles: tuple[int, int, int], a: np.ndarray, b: np.ndarray, repeat: int = 2, number: int = 1,
+                  min_repeat_ms: int = 50) -> float:
+    """Seconds per call of one compiled schedule (min over repeats), with the
+    reference's evaluate_perf when oracle/_ref is built."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib = schedule_lib(*tiles)
+    lib.xtc_cpu_sched_configure(m, n, k)
+    ref = ref_runtime()
+    fn = ctypes.cast(lib.xtc_cpu_sched_payload, ctypes.c_void_p)
+    if ref is not None:
+        results = (ctypes.c_double * repeat)()
+        args = (ctypes.c_void_p * 3)(a.ctypes.data, b.ctypes.data, c.ctypes.data)
+        ref.evaluate_perf(results, 0, None, repeat, number, min_repeat_ms, fn, args, 3)
+        return float(min(results))
+    payload = lib.xtc_cpu_sched_payload
+    payload.argtypes = [ctypes.c_void_p] * 3
+    return time_call(lambda: payload(a.ctypes.data, b.ctypes.data, c.ctypes.data), repeat, min_repeat_ms)
+
+
+def autoschedule_tile_oo(n: int, trials: int = 64, seed: int = 0, bf16: bool = False,
+                         jobs: int = 8) -> tuple[tuple[int, int, int], float, int]:
+    """loop-explore of the restatement: `trials` seeded random samples of the
+    reference's tile_oo strategy (src/xtc/search/strategies.py:739-758,
+    restated in xtc_amd/search/strategies.py) for an n^3 fp32 matmul, each
+    compiled as its own object and timed with the evaluate_perf protocol.
+    Returns (best (i1, k1, j1), its seconds per call, samples timed)."""
+    import concurrent.futures as cf
+
+    from xtc_amd.cli.explore import build_graph
+    from xtc_amd.search.strategies import Strategies
+
+    graph = build_graph("matmul", [n, n, n], "float32")
+    strategy = Strategies.create("tile_oo", graph, threads=threads())
+    names = strategy.sample_names
+    samples = [dict(zip(names, x)) for x in strategy.sample(trials, seed=seed)]
+    # tile_oo's sample is (i1, j1, k1); the restatement takes (i1, k1, j1)
+    tiles = [(x[names[0]], x[names[2]], x[names[1]]) for x in samples]
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(lambda t: schedule_lib(*t), tiles))
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    if bf16:
+        from xtc_amd.utils.bf16 import round_to_bf16
+
+        a, b = round_to_bf16(a), round_to_bf16(b)
+    timed = [(time_schedule(t, a, b, repeat=1, min_repeat_ms=20), t) for t in tiles]
+    t, best = min(timed)
+    return best, t, len(timed)
 
 
 def autoschedule_matmul(a: np.ndarray, b: np.ndarray, repeat: int = 2, min_repeat_ms: int = 50) -> tuple[int, float]:

@@ -348,3 +348,15 @@ def test_measured_mfma_peak():
         for v in (ref_ops, zero, rand):
             assert 0.4 * sheet < v <= 1.02 * sheet
         assert zero >= 0.97 * rand
+
+
+@pytest.mark.parametrize("opname", ["matmul", "conv2d"])
+def test_reference_graph_files_validate(opname):
+    # the reference's tests/graphs/*.graph.yaml, run with XTC's validation
+    from pathlib import Path
+
+    with O.graph() as gb:
+        gb.load(Path(__file__).resolve().parent / "golden" / "graphs" / f"{opname}.graph.yaml")
+    module = _compile(gb.graph)
+    res, code, msg = module.get_evaluator(validate=True, repeat=1, number=1, min_repeat_ms=0).evaluate()
+    assert code == 0, msg

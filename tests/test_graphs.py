@@ -270,3 +270,36 @@ def test_graph_yaml_round_trip(tmp_path):
     assert canon(str(g2)) == canon(str(g))
     inps = _inputs([T.TensorType((2, 6, 6, 3), "float32"), T.TensorType((8, 5, 5, 3), "float32")])
     np.testing.assert_array_equal(g2.forward(inps)[0].numpy(), g.forward(inps)[0].numpy())
+
+
+# The reference's own graph files (tests/graphs/*.graph.yaml, loaded by
+# tests/pytest/graphs/test_graph_serialization.py:8-19), kept as data.
+REF_GRAPHS = Path(__file__).resolve().parent / "golden" / "graphs"
+
+
+@pytest.mark.parametrize("opname,ins,outs", [
+    ("matmul", ["512x128xfloat32", "128x1024xfloat32"], ["512x1024xfloat32"]),
+    ("conv2d", ["1x230x230x3xfloat32", "7x7x3x64xfloat32"], ["1x112x112x64xfloat32"]),
+])
+def test_reference_graph_files_load_and_compile(opname, ins, outs):
+    import yaml
+
+    from xtc_amd.backends.hip import Backend
+
+    path = REF_GRAPHS / f"{opname}.graph.yaml"
+    with O.graph() as gb:
+        gb.load(path)
+    graph = gb.graph
+    assert graph.name == opname
+    assert [str(t) for t in graph.inputs_types] == ins and [str(t) for t in graph.outputs_types] == outs
+    # the same document back, but for the digest of the operator classes
+    # (ops_version hashes the registering module's names)
+    data = yaml.safe_load(path.read_text())
+    mine = graph.to_dict()
+    assert {k: v for k, v in mine.items() if k != "ops_version"} == {k: v for k, v in data.items() if k != "ops_version"}
+    with O.graph() as gb2:
+        gb2.loads(graph.dumps())
+    assert gb2.graph.to_dict() == mine
+    backend = Backend(graph)
+    module = backend.get_compiler().compile(backend.get_scheduler().schedule())
+    assert module.schedule_error is None and len(module.configs) == 1

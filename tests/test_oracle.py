@@ -215,3 +215,22 @@ def test_c5_integer_rounding_is_order_dependent(cpu):
     assert np.allclose(seq, blas, rtol=1e-4)
     assert np.allclose(seq, exact, rtol=1e-4)
     assert np.allclose(blas, exact, rtol=1e-4)
+
+
+def test_cpu_backend_single_schedule_builds_are_exact():
+    # one compiled object per sampled tile_oo schedule (i1, k1, j1), ragged
+    # against the shape: exact on integer inputs like the fixed variants
+    import ctypes
+
+    from oracle import cpu_baseline as cb
+
+    a = R.np_init((37, 70), "float32")
+    b = R.np_init((70, 45), "float32")
+    want = R.matmul(a, b).astype(np.float32)
+    for tiles in [(1, 1, 8), (2, 4, 16), (8, 64, 32), (5, 3, 7)]:
+        lib = cb.schedule_lib(*tiles)
+        lib.xtc_cpu_sched_configure(37, 45, 70)
+        c = np.full((37, 45), np.nan, np.float32)
+        lib.xtc_cpu_sched_payload.argtypes = [ctypes.c_void_p] * 3
+        lib.xtc_cpu_sched_payload(a.ctypes.data, b.ctypes.data, c.ctypes.data)
+        np.testing.assert_array_equal(c, want, err_msg=str(tiles))
