@@ -431,7 +431,7 @@ def test_pipeline_depth_queries():
     d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32, M=100, N=60, K=30)
     assert capi.matmul_pipeline_depths(d) == [1]  # K and N not multiples of the 4-element vector: scalar kernel
     d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32, M=512, N=512, K=512, tile=capi.Tile(32, 32, 16, 1, 1), split_k=4)
-    assert capi.matmul_pipeline_depths(d) == [4]  # split-wave register ring
+    assert capi.matmul_pipeline_depths(d) == [4, 2, 8]  # split-wave register ring
     d = capi.MatmulDesc(dtype=capi.XTC_HIP_BF16, M=512, N=512, K=512, tile=capi.Tile(256, 256, 32, 2, 4), trans_b=1)
     assert capi.matmul_pipeline_depths(d) == [4, 3, 5]  # B^T read natively by the ping-pong kernel
     c = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=8, H=56, W=56, C=64, F=64, R=3, S=3, stride_h=1, stride_w=1,

@@ -810,6 +810,10 @@ DEPTH_CASES = [
     ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 256, 224), True),
     ("bfloat16", (16, 128, 64, 1, 4), 8, (16, 1024, 8192), False),
     ("bfloat16", (16, 128, 64, 1, 4), 8, (12, 1024, 4096), False),
+    # split-wave register ring: 8 chunks per wave, then 3 and 5 (not multiples of the depth)
+    ("float32", (32, 32, 16, 1, 1), 4, (512, 512, 512), False),
+    ("float32", (32, 32, 16, 1, 1), 4, (64, 96, 192), False),
+    ("float32", (32, 32, 16, 1, 1), 3, (96, 64, 240), False),
 ]
 
 

@@ -754,7 +754,21 @@ bool splitwave_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t,
   return true;
 }
 
-int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, int ldb, int ldc,
+// Pipeline depths (register ring chunks) of the split-wave kernel, default
+// first.
+constexpr int kSplitWaveDepths[] = {4, 2, 8};
+
+template <int S>
+void launch_splitwave_s(int depth, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  if (depth == 2)
+    hipLaunchKernelGGL((gemm_f32_splitwave<S, 2>), grid, dim3(S * 64), 0, s, a);
+  else if (depth == 4)
+    hipLaunchKernelGGL((gemm_f32_splitwave<S, 4>), grid, dim3(S * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_f32_splitwave<S, 8>), grid, dim3(S * 64), 0, s, a);
+}
+
+int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int stages, int lda, int ldb, int ldc,
                           const void* A, const void* B, float* C, const float* bias, hipStream_t s) {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
@@ -776,20 +790,16 @@ int launch_splitwave_gemm(const xtc_hip_matmul_desc& d, int split_k, int lda, in
   a.xcd_remap = d.xcd_remap;
   a.k_per_split = d.K / split_k;
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (split_k == 2)
-    hipLaunchKernelGGL((gemm_f32_splitwave<2>), grid, dim3(128), 0, s, a);
-  else if (split_k == 3)
-    hipLaunchKernelGGL((gemm_f32_splitwave<3>), grid, dim3(192), 0, s, a);
-  else if (split_k == 4)
-    hipLaunchKernelGGL((gemm_f32_splitwave<4>), grid, dim3(256), 0, s, a);
-  else if (split_k == 5)
-    hipLaunchKernelGGL((gemm_f32_splitwave<5>), grid, dim3(320), 0, s, a);
-  else if (split_k == 6)
-    hipLaunchKernelGGL((gemm_f32_splitwave<6>), grid, dim3(384), 0, s, a);
-  else if (split_k == 7)
-    hipLaunchKernelGGL((gemm_f32_splitwave<7>), grid, dim3(448), 0, s, a);
-  else
-    hipLaunchKernelGGL((gemm_f32_splitwave<8>), grid, dim3(512), 0, s, a);
+  const int depth = stages > 0 ? stages : kSplitWaveDepths[0];
+  switch (split_k) {
+    case 2: launch_splitwave_s<2>(depth, grid, a, s); break;
+    case 3: launch_splitwave_s<3>(depth, grid, a, s); break;
+    case 4: launch_splitwave_s<4>(depth, grid, a, s); break;
+    case 5: launch_splitwave_s<5>(depth, grid, a, s); break;
+    case 6: launch_splitwave_s<6>(depth, grid, a, s); break;
+    case 7: launch_splitwave_s<7>(depth, grid, a, s); break;
+    default: launch_splitwave_s<8>(depth, grid, a, s); break;
+  }
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -1059,7 +1069,7 @@ int path_depths(MatmulPath p, const xtc_hip_tile& t, int* out, int max) {
       tmp[n++] = 2;
       break;
     case MatmulPath::SplitWave:
-      tmp[n++] = 4;
+      for (int v : kSplitWaveDepths) tmp[n++] = v;
       break;
     case MatmulPath::F32Lds:
       for (const F32LdsVariant& v : kF32Lds)
@@ -1187,7 +1197,8 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   }
   if (path == MatmulPath::LdsDma) return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, false);
   if (path == MatmulPath::Skinny) return launch_skinny_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x);
-  if (path == MatmulPath::SplitWave) return launch_splitwave_gemm(d, split_k, lda, ldb, ldc, A, B, C, bias, s);
+  if (path == MatmulPath::SplitWave)
+    return launch_splitwave_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, s);
   const GemmEntry* e = find_entry(d.dtype, 0, t);
   GemmEntry lds_entry;
   if (path == MatmulPath::F32Lds) {
