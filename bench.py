@@ -171,8 +171,8 @@ def _elementwise(steps: int) -> int:
     the bf16 casts (library entry points) and the transpose that stages a
     transposed matmul operand (timed inside a trans_a matmul with N = 16, so
     its rate is read from the kernel trace: the line's time includes the
-    skinny GEMM).  Bytes are algorithmic: every input element read once, every
-    output element written once."""
+    generic GEMM that consumes the copy).  Bytes are algorithmic: every input
+    element read once, every output element written once."""
     import numpy as np
 
     from xtc_amd.runtimes.hip import capi
@@ -219,7 +219,7 @@ def _elementwise(steps: int) -> int:
     for dtype, esz in (("float32", 4), ("bfloat16", 2)):
         d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, M=8192, N=16,
                             K=8192, trans_a=1, xcd_remap=1)
-        timed(f"matmul trans_a {dtype} 8192x16x8192 (transpose_kernel + skinny GEMM)", 2 * esz * 8192 * 8192,
+        timed(f"matmul trans_a {dtype} 8192x16x8192 (transposed copy + generic GEMM)", 2 * esz * 8192 * 8192,
               lambda d=d: capi.check(L.xtc_hip_matmul(ctypes.byref(d), xp, yp, hp, None), "matmul"))
     capi.check(L.xtc_hip_synchronize(), "synchronize")
     return 0

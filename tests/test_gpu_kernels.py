@@ -473,7 +473,11 @@ def test_matmul_operand_layouts_integer_exact(dtype, ta, tb):
     # generic template (ragged and aligned shapes, split-K), the skinny bf16
     # kernel and the LDS-DMA kernel (B^T read natively, A^T via a transposed
     # copy); padded leading dimensions on the stored matrices
-    cases = [((64, 96, 128), None, 0, 0, 0), ((70, 130, 200), None, 0, 8, 4), ((96, 160, 2048), None, 4, 0, 0)]
+    # transposed copies: 16-byte vectors when the stored dims are multiples
+    # of the vector (ragged against the 64/128-element tile: 96, 136, 264),
+    # element by element otherwise (70, 130, ld 100 for bf16)
+    cases = [((64, 96, 128), None, 0, 0, 0), ((70, 130, 200), None, 0, 8, 4), ((96, 160, 2048), None, 4, 0, 0),
+             ((136, 96, 264), None, 0, 0, 0)]
     if dtype == "bfloat16":
         cases += [((256, 512, 256), (256, 256, 64, 2, 4), 0, 0, 0), ((512, 256, 320), (256, 256, 64, 4, 2), 0, 16, 8),
                   ((16, 1024, 8192), (16, 128, 64, 1, 4), 8, 0, 0)]
