@@ -436,7 +436,7 @@ def test_pipeline_depth_queries():
     assert capi.matmul_pipeline_depths(d) == [4, 3, 5]  # B^T read natively by the ping-pong kernel
     c = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=8, H=56, W=56, C=64, F=64, R=3, S=3, stride_h=1, stride_w=1,
                         pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)
-    assert capi.conv2d_pipeline_depths(c) == [3]  # direct conv: 3 weight-tap stages
+    assert capi.conv2d_pipeline_depths(c) == [3]  # direct conv 8x14: a register ring of 3 weight taps
     d = capi.MatmulDesc(dtype=7, M=1, N=1, K=1)
     with pytest.raises(capi.HipError, match="bad dtype"):
         capi.matmul_pipeline_depths(d)

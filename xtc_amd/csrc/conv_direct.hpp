@@ -15,12 +15,21 @@
 //   * the input halo ((TH-1)*sh+R) x ((TW-1)*sw+S) pixels x 64 channels is
 //     loaded once into LDS (pad_value outside the image), pixel stride 68
 //     floats so the 16 pixels read by a lane group fall on distinct banks;
-//   * the weights stream one tap (r, s) [64 c][64 f] = 16 KB at a time
-//     through 3 LDS stages by LDS DMA (issued from asm, lds_dma.hpp, so the
-//     compiler's waits on the LDS operand reads stay exact), two taps
-//     ahead; the 16-byte chunks of
-//     weight row c are XOR-swizzled by 4*((c>>2)&3) so the scalar B reads of
-//     the four lane groups hit disjoint banks;
+//   * the weights take one of two paths (template parameter WRING):
+//     - WRING = 0: they stream one tap (r, s) [64 c][64 f] = 16 KB at a time
+//       through 3 LDS stages by LDS DMA (issued from asm, lds_dma.hpp, so
+//       the compiler's waits on the LDS operand reads stay exact), two taps
+//       ahead, behind a barrier per tap; the 16-byte chunks of weight row c
+//       are XOR-swizzled by 4*((c>>2)&3) so the scalar B reads of the four
+//       lane groups hit disjoint banks;
+//     - WRING > 0: each lane loads its own B fragments of a tap (16 FT
+//       floats: its filter column, the 16 channels its MFMA k-slots take)
+//       straight from global memory into a ring of WRING taps of registers,
+//       WRING taps ahead of the MFMAs.  No weight LDS, no DMA and no
+//       barrier inside the K walk; the only barrier publishes the halo.
+//       With one wave per SIMD (8x14 blocks: FT = 1) it is 6 % faster than
+//       the LDS stages; with FT = 2 (8x8 blocks) 5 % slower, the twice as
+//       many 4-byte loads per tap outweighing the saved barriers;
 //   * 4 waves (WM x WN), each TH*TW/WM pixels x 64/WN filters of
 //     v_mfma_f32_16x16x4_f32; the filter fragment is the first operand, so a
 //     lane ends up with 4 consecutive filters of one pixel and stores a float4;
@@ -71,18 +80,23 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n 
 }  // namespace dconv
 
 // TH x TW output pixels per workgroup, WM x WN waves, HALO_BYTES of LDS for
-// the input halo of one 64-channel chunk.
-template <int TH, int TW, int WM, int WN, int HALO_BYTES>
+// the input halo of one 64-channel chunk, weights through LDS stages
+// (WRING = 0) or a register ring of WRING taps.
+template <int TH, int TW, int WM, int WN, int HALO_BYTES, int WRING>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_direct_f32(DirectConvArgs a) {
   using namespace dconv;
   constexpr int HALO_MAX_PIX = halo_pix(HALO_BYTES);
   constexpr int PT = TH * TW / 16 / WM;  // 16-pixel tiles per wave
   constexpr int FT = FB / WN / 16;       // 16-filter tiles per wave
+  constexpr bool REG = WRING > 0;
+  constexpr int RING = REG ? WRING : STAGES;  // slabs in flight + 1 (LDS) or in registers
+  constexpr int WBYTES = REG ? 16 : W_STAGE;
   static_assert(WM * WN == NW && TH * TW % (16 * WM) == 0 && FB % (16 * WN) == 0, "tiling");
+  static_assert(WRING >= 0 && WRING <= 4, "register ring");
   __shared__ __attribute__((aligned(1024))) float halo[HALO_MAX_PIX * CP];
-  __shared__ __attribute__((aligned(1024))) unsigned char w0[W_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char w1[W_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char w2[W_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char w0[WBYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char w1[WBYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char w2[WBYTES];
   unsigned char* const wst[3] = {w0, w1, w2};
 
   const int tid = threadIdx.x;
@@ -127,6 +141,21 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     for (int i = 0; i < DMA_PER_WAVE; ++i)
       lds_dma16((const void*)(base + (size_t)w_row[i] * a.F + w_col[i]), st + (wave * DMA_PER_WAVE + i) * 1024);
   };
+  // register ring: lane (l16, g) holds
+  // W[r][s][chunk*64 + 16 kc + 4 g + st][fb*64 + wn*16*FT + 16 jt + l16]
+  float wr[REG ? RING : 1][CB / 16][4][FT];
+  const float* const wlane = a.Wt + (size_t)(4 * g) * a.F + fb * FB + wn * 16 * FT + l16;
+  auto load_slab = [&](int t, const int u) {
+    const int chunk = t / taps;
+    const int tap = t - chunk * taps;
+    const float* base = wlane + ((size_t)tap * a.C + chunk * CB) * a.F;
+#pragma unroll
+    for (int kc = 0; kc < CB / 16; ++kc)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int jt = 0; jt < FT; ++jt) wr[u][kc][st][jt] = base[(size_t)(kc * 16 + st) * a.F + jt * 16];
+  };
 
   // All of a thread's halo loads are issued before its first LDS write (at
   // most HALO_MAX_PIX * 16 / 256 chunks: 8 for 8x8 tiles, 12 for 8x14), so
@@ -168,9 +197,15 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
 #pragma unroll
     for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  if constexpr (REG) {
 #pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
-    if (t < nslab) issue_slab(t, wst[t]);
+    for (int t = 0; t < RING; ++t)
+      if (t < nslab) load_slab(t, t);
+  } else {
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+      if (t < nslab) issue_slab(t, wst[t]);
+  }
 
   auto step = [&](int t, const int s) {
     const int chunk = t / taps;
@@ -179,13 +214,17 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
       if (chunk > 0) __syncthreads();  // every wave is done with the previous chunk's halo
       load_halo(chunk);
     }
-    if (t + STAGES - 2 < nslab)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * DMA_PER_WAVE));
-    else
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    __syncthreads();  // slab t (and the halo) visible; stage of slab t-1 free
-    if (t + STAGES - 1 < nslab) issue_slab(t + STAGES - 1, wst[(s + STAGES - 1) % STAGES]);
-    const float* ws = (const float*)wst[s];
+    if constexpr (REG) {
+      if (tap == 0) __syncthreads();  // halo visible
+    } else {
+      if (t + STAGES - 2 < nslab)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * DMA_PER_WAVE));
+      else
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      __syncthreads();  // slab t (and the halo) visible; stage of slab t-1 free
+      if (t + STAGES - 1 < nslab) issue_slab(t + STAGES - 1, wst[(s + STAGES - 1) % STAGES]);
+    }
+    const float* ws = (const float*)wst[REG ? 0 : s];
     const int r = tap / a.S;
     const int sx = tap - r * a.S;
     int aoff[PT];
@@ -202,17 +241,20 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
 #pragma unroll
         for (int jt = 0; jt < FT; ++jt) {
           const int f = wn * 16 * FT + jt * 16 + l16;
-          const float bv = ws[c * FB + ((f >> 2) ^ swz(c)) * 4 + (f & 3)];
+          const float bv = REG ? wr[REG ? s : 0][kc][st][jt] : ws[c * FB + ((f >> 2) ^ swz(c)) * 4 + (f & 3)];
 #pragma unroll
           for (int it = 0; it < PT; ++it)
             acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av[it][st], acc[it][jt], 0, 0, 0);
         }
       }
     }
+    if constexpr (REG) {
+      if (t + RING < nslab) load_slab(t + RING, s);
+    }
   };
-  for (int t = 0; t < nslab; t += STAGES) {
+  for (int t = 0; t < nslab; t += RING) {
 #pragma unroll
-    for (int s = 0; s < STAGES; ++s)
+    for (int s = 0; s < RING; ++s)
       if (t + s < nslab) step(t + s, s);
   }
 

@@ -464,20 +464,25 @@ int grid_for(uint64_t n, int block) {
 // waves, and the LDS of the input halo.  8x8 (2x2 waves) shares its tile
 // with a generic implicit-GEMM instance, which runs the shapes the direct
 // kernel does not take; 8x14 (1x4 waves, 224 equal blocks for 8x56x56
-// outputs: one per CU) exists only here.
+// outputs: one per CU) exists only here.  8x8 streams its weights through
+// LDS stages, 8x14 through a register ring of 3 taps (the faster path for
+// each in one process).
 typedef void (*DirectConvLaunch)(const DirectConvArgs&, dim3, hipStream_t);
-template <int TH, int TW, int WM, int WN, int HALO_BYTES>
+template <int TH, int TW, int WM, int WN, int HALO_BYTES, int WRING>
 void launch_conv_direct(const DirectConvArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((conv_direct_f32<TH, TW, WM, WN, HALO_BYTES>), grid, dim3(dconv::NT), 0, s, a);
+  hipLaunchKernelGGL((conv_direct_f32<TH, TW, WM, WN, HALO_BYTES, WRING>), grid, dim3(dconv::NT), 0, s, a);
 }
 struct DirectConvTile {
   xtc_hip_tile tile;
   int th, tw, halo_bytes;
+  int wring;  // 0: weights through dconv::STAGES LDS stages, else register ring depth
   DirectConvLaunch launch;
+  int lds_bytes() const { return halo_bytes + (wring ? 0 : dconv::STAGES * dconv::W_STAGE); }
+  int depth() const { return wring ? wring : dconv::STAGES; }
 };
 const DirectConvTile kDirectConv[] = {
-    {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, &launch_conv_direct<8, 8, 2, 2, 32 * 1024>},
-    {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, &launch_conv_direct<8, 14, 1, 4, 48 * 1024>},
+    {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, 0, &launch_conv_direct<8, 8, 2, 2, 32 * 1024, 0>},
+    {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, 3, &launch_conv_direct<8, 14, 1, 4, 48 * 1024, 3>},
 };
 
 bool same_tile(const xtc_hip_tile& a, const xtc_hip_tile& b) {
@@ -504,7 +509,7 @@ const GemmEntry* direct_only_entries(int* n) {
                               same_tile(xtc_hip_tile{e[i].bm, e[i].bn, e[i].bk, e[i].wgm, e[i].wgn}, d.tile));
       if (!generic)
         out.push_back(GemmEntry{XTC_HIP_F32, 1, d.tile.bm, d.tile.bn, d.tile.bk, d.tile.wgm, d.tile.wgn,
-                                d.halo_bytes + dconv::STAGES * dconv::W_STAGE, dconv::NT, nullptr});
+                                d.lds_bytes(), dconv::NT, nullptr});
     }
     return out;
   }();
@@ -1605,10 +1610,10 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
     return -fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype, t.bm, t.bn, t.bk,
                  t.wgm, t.wgn);
   const void* p = (const void*)(uintptr_t)256;
-  // the direct kernel streams the weight taps through dconv::STAGES stages;
-  // the implicit-GEMM loader double-buffers through registers
+  // the direct kernel keeps its weight taps in LDS stages or a register
+  // ring; the implicit-GEMM loader double-buffers through registers
   if (direct_conv_applies(d, t, split_k, OH, OW, p, p, p, nullptr))
-    depths[0] = dconv::STAGES;
+    depths[0] = direct_conv_tile(t)->depth();
   else if (e->launch)
     depths[0] = 2;
   else
