@@ -356,6 +356,93 @@ def test_unmapped_schedule_fails_at_evaluation_by_default():
     assert nearest.schedule_error is None and not nearest.configs["C"].exact
 
 
+def _split_schedule(b):
+    """i split at 256 into two segments with their own tiles; the second
+    segment's j split again at 128 (nested), each piece with its own tile
+    (src/xtc/itf/schd/scheduler.py:65-81: segments by ascending start)."""
+    sch = b.get_scheduler()
+    sch.split("i", {"i_lo": 0, "i_hi": 256})
+    sch.tile("i", {"i1": 128, "i2": 64}, root="./i_lo")
+    sch.tile("j", {"j1": 128, "j2": 64}, root="./i_lo")
+    sch.tile("k", {"k1": 32}, root="./i_lo")
+    sch.split("j", {"j_a": 0, "j_b": 128}, root="./i_hi")
+    sch.tile("i", {"i1": 64}, root="./i_hi/j_a")
+    sch.tile("j", {"j1": 64}, root="./i_hi/j_a")
+    sch.tile("k", {"k1": 32}, root="./i_hi/j_a")
+    return sch
+
+
+def test_split_maps_to_one_launch_per_segment():
+    from xtc_amd.backends.hip.mapping import SplitConfig, map_node
+
+    b = Backend(_matmul(384, 256, 512))
+    sch = _split_schedule(b)
+    (ln,) = b.plan.launches
+    cfg = map_node(ln.attrs, False, sch.schedule().node(ln.node))
+    assert isinstance(cfg, SplitConfig) and cfg.exact
+    got = [(p.m0, p.M, p.n0, p.N, p.config.tile[:3], p.config.source) for p in cfg.pieces]
+    assert got == [
+        (0, 256, 0, 256, (128, 128, 32), "schedule"),
+        (256, 128, 0, 128, (64, 64, 32), "schedule"),
+        (256, 128, 128, 128, _default_tile_of(128, 128, 512), "default"),  # untiled segment
+    ]
+    # one launch per piece on the strided sub-views, whole-operand strides
+    module = b.get_compiler().compile(sch.schedule())
+    body = module.source.split(f"void {module.payload_name}(")[-1]
+    assert body.count("xtc_hip_matmul(") == 3
+    assert "(const char *)a0 + 524288ull" in body  # A rows from 256: 256 * 512 * 4 bytes
+    assert "(const char *)a1 + 512ull" in body  # B columns from 128
+    assert "(char *)a2 + 262656ull" in body  # C at (256, 128): (256 * 256 + 128) * 4
+    assert re.search(r"= \{XTC_HIP_F32, 128, 128, 512, 512, 256, 256, ", body)
+
+
+def _default_tile_of(m, n, k):
+    tile, _ = capi.default_tile("float32", False, m, n, k)
+    return tuple(tile[:3])
+
+
+def test_split_transposed_operands_offset_the_other_way():
+    from xtc_amd.backends.hip.mapping import SplitConfig
+
+    a = O.tensor((256, 128), "float32", name="A", layout=[1, 0])
+    bt = O.tensor((128, 256), "float32", name="B", layout=[1, 0])
+    with O.graph(name="mmt") as gb:
+        O.matmul(a, bt, name="C")
+    b = Backend(gb.graph)
+    sch = b.get_scheduler()
+    sch.split("i", {"lo": 0, "hi": 64})
+    sch.split("j", {"l": 0, "r": 32}, root="./hi")
+    module = b.get_compiler().compile(sch.schedule())
+    assert isinstance(module.configs["C"], SplitConfig)
+    body = module.source.split(f"void {module.payload_name}(")[-1]
+    # A^T [128][256]: rows 64.. of A are columns 64.. of A^T (64 * 4 bytes);
+    # B^T [256][128]: columns 32.. of B are rows 32.. of B^T (32 * 128 * 4)
+    assert "(const char *)a0 + 256ull" in body and "(const char *)a1 + 16384ull" in body
+    assert re.search(r"= \{XTC_HIP_F32, 192, 32, 128, 256, 128, 256, ", body)
+
+
+def test_split_on_k_or_conv_is_rejected():
+    from xtc_amd.backends.hip.mapping import map_node
+
+    b = Backend(_matmul(256, 256, 512))
+    sch = b.get_scheduler()
+    sch.split("k", {"k_lo": 0, "k_hi": 256})
+    (ln,) = b.plan.launches
+    with pytest.raises(ScheduleError, match="reduction axis"):
+        map_node(ln.attrs, False, sch.schedule().node(ln.node))
+    sch = b.get_scheduler()
+    sch.split("i", {"a": 64, "b": 128})
+    with pytest.raises(ScheduleError, match="starts at 64"):
+        map_node(ln.attrs, False, sch.schedule().node(ln.node))
+    g = _conv_relu()
+    bc = Backend(g)
+    sch = bc.get_scheduler()
+    (cl,) = [l for l in bc.plan.launches if l.kind == "conv2d"]
+    sch.split(sch.schedule().node(cl.node).dims[0], {"x": 0, "y": 4})
+    with pytest.raises(ScheduleError, match="conv2d"):
+        map_node(cl.attrs, True, sch.schedule().node(cl.node))
+
+
 def test_mapping_split_k():
     attrs, s = _sched(_matmul(256, 256, 8192), {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 1024, "k2": 32}},
                       parallel=["k"])

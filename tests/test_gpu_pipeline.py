@@ -332,6 +332,67 @@ def test_operand_layouts_seeded_logical_parameters():
     assert ref.scaled_error(out, ref.matmul(a, b), 1024, 1.0, 1.0) <= TOL_BF16
 
 
+# split() of i or j: one launch per segment on strided sub-views, each segment
+# with its own tiles (src/xtc/itf/schd/scheduler.py:65-81)
+SPLIT_CASES = [
+    # (dtype, layouts, M, N, K, i cut, j cut in the second i segment, relu)
+    ("float32", (False, False), 384, 256, 512, 256, 128, True),
+    ("float32", (True, True), 300, 200, 96, 100, 36, False),  # ragged, offsets not 16-byte aligned
+    ("bfloat16", (False, True), 512, 512, 256, 256, 256, False),  # B^T read natively per piece
+    ("bfloat16", (True, False), 96, 1024, 8192, 16, 512, True),  # skinny first piece
+]
+
+
+def _split_graph(dtype, layouts, m, n, k, relu):
+    a = O.tensor((m, k), dtype, name="A", layout=[1, 0] if layouts[0] else None)
+    b = O.tensor((k, n), dtype, name="B", layout=[1, 0] if layouts[1] else None)
+    with O.graph(name="matmul_split") as gb:
+        c = O.matmul(a, b, name="C", **({"out_dtype": "float32"} if dtype == "bfloat16" else {}))
+        if relu:
+            O.relu(c, name="relu")
+    return gb.graph
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"{c[0]}-{c[2]}x{c[3]}x{c[4]}-ta{int(c[1][0])}tb{int(c[1][1])}"
+                                                   for c in SPLIT_CASES])
+def test_split_schedule_parity(case):
+    from xtc_amd.backends.hip.mapping import SplitConfig
+
+    dtype, layouts, m, n, k, icut, jcut, relu = case
+    print(f"[split] {case}", flush=True)
+    backend = Backend(_split_graph(dtype, layouts, m, n, k, relu))
+    sch = backend.get_scheduler()
+    sch.split("i", {"i_lo": 0, "i_hi": icut})
+    if icut <= 16:
+        tiles = {}  # the library default: the skinny bf16 kernel
+    elif dtype == "bfloat16" and m >= 256 and icut % 256 == 0:
+        tiles = {"i": {"i1": 256, "i2": 128}, "j": {"j1": 256, "j2": 64}, "k": {"k1": 32}}
+    else:
+        tiles = {"i": {"i1": 64}, "j": {"j1": 64}, "k": {"k1": 32 if dtype == "float32" else 64}}
+    for dim, t in tiles.items():
+        sch.tile(dim, t, root="./i_lo")
+    sch.split("j", {"j_a": 0, "j_b": jcut}, root="./i_hi")
+    sch.tile("i", {"i1": 32}, root="./i_hi/j_b")
+    sch.tile("j", {"j1": 32}, root="./i_hi/j_b")
+    sch.tile("k", {"k1": 16 if dtype == "float32" else 32}, root="./i_hi/j_b")
+    module = backend.get_compiler().compile(sch.schedule())
+    cfg = module.configs["C"]
+    assert isinstance(cfg, SplitConfig) and len(cfg.pieces) == 3, cfg
+    rng = np.random.default_rng(5)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    if dtype == "bfloat16":
+        a, b = ref.round_bf16(a), ref.round_bf16(b)
+    (out,) = _run(module, [a, b])
+    want = ref.matmul(a, b)
+    if relu:
+        want = np.maximum(want, 0.0)
+    assert ref.scaled_error(out, want, k, 1.0, 1.0) <= (TOL_F32 if dtype == "float32" else TOL_BF16)
+    # integer inputs: every piece exact, the XTC validation path included
+    res, code, msg = module.get_evaluator(validate=True, repeat=1, number=1, min_repeat_ms=0).evaluate()
+    assert code == 0, msg
+
+
 def test_measured_mfma_peak():
     # the register-only MFMA probe behind evaluate_flops (FMA/s): at most the
     # datasheet peak, and zeros run at least as fast as random operands

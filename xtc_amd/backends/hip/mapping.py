@@ -33,6 +33,11 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
   * pack_at(local), buffer_at, fuse_producer_at -> always on in these
     kernels (LDS staging of both operands, register-resident output tile,
     pad folded into the conv loader); recorded, no further effect.
+  * split(i or j, segments) of a matmul -> one launch per segment on the
+    strided sub-view of A (rows) or B (columns), C and bias, each mapped from
+    its own root's tiles and knobs (src/xtc/itf/schd/scheduler.py:65-81); a
+    split on the reduction axis, or on a conv2d, is rejected: the kernels
+    overwrite C rather than accumulate into it.
 
 Tile semantics follow the reference: a tile size is the extent of the
 sub-loop (src/xtc/backends/mlir/MlirCompilerPasses.py:414-457).
@@ -54,7 +59,7 @@ from typing import Any
 
 from .scheduler import HipNodeSchedule, ScheduleError
 
-__all__ = ["GemmConfig", "map_gemm", "gemm_instances", "legal_tiles", "pipeline_depths"]
+__all__ = ["GemmConfig", "SplitConfig", "map_gemm", "map_node", "gemm_instances", "legal_tiles", "pipeline_depths"]
 
 DEFAULT_GROUP_M = 8
 
@@ -85,6 +90,32 @@ class GemmConfig:
             f"{'conv' if self.conv else 'gemm'}<{self.dtype}> BMxBNxBK={self.bm}x{self.bn}x{self.bk} "
             f"waves={self.wgm}x{self.wgn} split_k={self.split_k}{depth} group_m={self.group_m} ({self.source})"
         )
+
+
+@dataclass(frozen=True)
+class SplitPiece:
+    """One launch of a split matmul: output rows [m0, m0 + M) and columns
+    [n0, n0 + N) on the kernel instance `config`."""
+
+    m0: int
+    M: int
+    n0: int
+    N: int
+    config: GemmConfig
+
+
+@dataclass(frozen=True)
+class SplitConfig:
+    """A matmul whose schedule splits i or j: one launch per piece."""
+
+    pieces: tuple[SplitPiece, ...]
+
+    @property
+    def exact(self) -> bool:
+        return all(p.config.exact for p in self.pieces)
+
+    def describe(self) -> str:
+        return "; ".join(f"rows {p.m0}+{p.M} cols {p.n0}+{p.N}: {p.config.describe()}" for p in self.pieces)
 
 
 @lru_cache(maxsize=None)
@@ -230,11 +261,11 @@ def map_gemm(
     cands = legal_tiles(dtype, conv)
     if not cands:
         raise ScheduleError(f"no compiled {'conv' if conv else 'matmul'} instance for {dtype}")
+    if sched is not None and sched.segments:
+        raise ScheduleError(f"{sched.node_name}: split() maps to several launches (map_node)")
     if sched is None or not any(sched.levels(d) for d in sched.dims) and not sched.parallelization:
         tile, split = _default(dtype, conv, M, N, K, launch_attrs)
         return GemmConfig(dtype, conv, *tile, split_k=split, exact=True, source="default")
-    if sched.splits:
-        raise ScheduleError(f"{sched.node_name}: split() has no HIP kernel mapping")
     m_dims, n_dims, k_dims = _dims_roles(sched, conv)
     bm = _level(sched, m_dims, 0)
     bn = _level(sched, n_dims, 0)
@@ -314,10 +345,58 @@ def map_gemm(
     return GemmConfig(dtype, conv, *tile, split_k=split_k, group_m=group_m, exact=False, source="nearest")
 
 
+def map_node(
+    launch_attrs: dict[str, Any],
+    conv: bool,
+    sched: HipNodeSchedule | None,
+    policy: str = "strict",
+) -> GemmConfig | SplitConfig:
+    """map_gemm, plus split() of a matmul's i or j axis into one launch per
+    segment (nested splits of a segment's own root included)."""
+    if sched is None or not sched.segments:
+        return map_gemm(launch_attrs, conv, sched, policy)
+    pieces = _split_pieces(launch_attrs, conv, sched, policy, 0, 0)
+    return SplitConfig(tuple(pieces))
+
+
+def _split_pieces(attrs: dict[str, Any], conv: bool, sched: HipNodeSchedule, policy: str, m0: int,
+                  n0: int) -> list[SplitPiece]:
+    if not sched.segments:
+        return [SplitPiece(m0, attrs["M"], n0, attrs["N"], map_gemm(attrs, conv, sched, policy))]
+    where = f"{sched.node_name}: split()"
+    if conv:
+        raise ScheduleError(f"{where} has no HIP mapping for conv2d (one launch covers the whole tensor)")
+    dims = {seg.dim for seg in sched.segments}
+    if len(dims) != 1:
+        raise ScheduleError(f"{where} of several axes at one root ({sorted(dims)}) has no HIP mapping")
+    (dim,) = dims
+    m_dim, n_dim, k_dim = sched.dims[0], sched.dims[1], sched.dims[2]
+    if dim == k_dim:
+        raise ScheduleError(f"{where} on the reduction axis {dim!r} has no HIP mapping: the kernels overwrite C "
+                            "rather than accumulate into it")
+    extent = attrs["M"] if dim == m_dim else attrs["N"]
+    segs = list(sched.segments)
+    if segs[0].start != 0:
+        raise ScheduleError(f"{where}: the first segment of {dim!r} starts at {segs[0].start}, not 0")
+    out: list[SplitPiece] = []
+    for seg in segs:
+        if not 0 <= seg.start < seg.end <= extent:
+            raise ScheduleError(f"{where}: segment [{seg.start}, {seg.end}) of {dim!r} is empty or outside "
+                                f"[0, {extent})")
+        sub = dict(attrs)
+        if dim == m_dim:
+            sub["M"] = seg.end - seg.start
+            out += _split_pieces(sub, conv, seg.schedule, policy, m0 + seg.start, n0)
+        else:
+            sub["N"] = seg.end - seg.start
+            out += _split_pieces(sub, conv, seg.schedule, policy, m0, n0 + seg.start)
+    return out
+
+
 def schedule_is_legal(sched: HipNodeSchedule, launch_attrs: dict[str, Any], conv: bool) -> bool:
     """True if `sched` maps exactly onto a compiled instance."""
     try:
-        return map_gemm(launch_attrs, conv, sched, policy="strict").exact
+        return map_node(launch_attrs, conv, sched, policy="strict").exact
     except ScheduleError:
         return False
 

@@ -27,7 +27,7 @@ from ...schedules.loop_nest import LoopNest, LoopNestNode, SplitOrigin
 if TYPE_CHECKING:
     from .backend import HipBackend
 
-__all__ = ["HipScheduler", "HipSchedule", "HipNodeSchedule", "ScheduleError"]
+__all__ = ["HipScheduler", "HipSchedule", "HipNodeSchedule", "HipSegment", "ScheduleError"]
 
 _SEP = "/"
 
@@ -44,6 +44,22 @@ def basename(name: str) -> str:
     return name.split(_SEP)[-1]
 
 
+def parent_of(name: str) -> str:
+    """The root a qualified loop or segment name lives in."""
+    return name.rsplit(_SEP, 1)[0]
+
+
+@dataclass(frozen=True)
+class HipSegment:
+    """One segment of a split() axis: [start, end) of `dim`, with the
+    schedule its root carries (re-rooted so its loops read as top-level)."""
+
+    dim: str
+    start: int
+    end: int
+    schedule: "HipNodeSchedule"
+
+
 @dataclass(frozen=True)
 class HipNodeSchedule:
     node_name: str
@@ -58,6 +74,8 @@ class HipNodeSchedule:
     packed_buffers: dict[str, list[int]]
     buffers: list[str]
     fused: list[tuple[str, int]]
+    # segments of the splits at the root, in axis order (empty without split)
+    segments: tuple[HipSegment, ...] = ()
 
     def levels(self, dim: str) -> list[int]:
         """Tile extents of `dim`, outer to inner (empty if untiled)."""
@@ -113,19 +131,47 @@ class _NodeScheduler:
     def freeze(self) -> HipNodeSchedule:
         if not self.permutation:
             self.permutation[DEFAULT_ROOT] = self.default_interchange(DEFAULT_ROOT)
+        return self._frozen_view(DEFAULT_ROOT, dict(self.sizes))
+
+    def _frozen_view(self, root: str, sizes: dict[str, int]) -> HipNodeSchedule:
+        """The schedule of the loops under `root`, renamed as if `root` were
+        the top level; the segments of the splits made at `root` carry the
+        views of their own roots."""
+
+        def under(name: str) -> bool:
+            return parent_of(name) == root
+
+        def rerooted(name: str) -> str:
+            return loop_name(DEFAULT_ROOT, basename(name))
+
+        splits = {d: v for d, v in self.splits.items() if v and all(under(seg) for seg in v)}
+        segments: list[HipSegment] = []
+        for dim, segs in splits.items():
+            names = list(segs)
+            for idx, seg in enumerate(names):
+                start = segs[seg]
+                end = segs[names[idx + 1]] if idx + 1 < len(names) else sizes[dim]
+                sub_sizes = dict(sizes)
+                sub_sizes[dim] = end - start
+                segments.append(HipSegment(dim, start, end, self._frozen_view(seg, sub_sizes)))
+        perm = self.permutation.get(root)
+        if perm is None:
+            perm = self.default_interchange(root) if root == DEFAULT_ROOT else []
         return HipNodeSchedule(
             node_name=self.node_name,
             dims=list(self.dims),
-            sizes=dict(self.sizes),
-            splits={k: dict(v) for k, v in self.splits.items()},
-            tiles={k: {basename(n): s for n, s in v.items()} for k, v in self.tiles.items() if k in self.dims},
-            permutation={k: list(v) for k, v in self.permutation.items()},
-            vectorization=list(self.vectorization),
-            parallelization=list(self.parallelization),
-            unrolling=dict(self.unrolling),
-            packed_buffers={k: list(v) for k, v in self.packed_buffers.items()},
-            buffers=list(self.buffers),
-            fused=list(self.fused),
+            sizes=dict(sizes),
+            splits={k: {basename(n): v for n, v in seg.items()} for k, seg in splits.items()},
+            tiles={k: {basename(n): s for n, s in v.items() if under(n)} for k, v in self.tiles.items()
+                   if k in self.dims},
+            permutation={DEFAULT_ROOT: [rerooted(p) for p in perm]},
+            vectorization=[rerooted(v) for v in self.vectorization if under(v)],
+            parallelization=[rerooted(v) for v in self.parallelization if under(v)],
+            unrolling={rerooted(k): v for k, v in self.unrolling.items() if under(k)},
+            packed_buffers={rerooted(k): list(v) for k, v in self.packed_buffers.items() if under(k)},
+            buffers=[rerooted(b) for b in self.buffers if under(b)],
+            fused=[(rerooted(a), i) for a, i in self.fused if under(a)],
+            segments=tuple(segments),
         )
 
 
@@ -270,11 +316,8 @@ class HipScheduler(Scheduler):
                 end = segs[names[idx + 1]] if idx + 1 < len(names) else None
                 segments[seg] = (dim, SplitOrigin(axis=dim, start=segs[seg], end=end))
 
-        def parent_of(qualified: str) -> str:
-            return qualified.rsplit("/", 1)[0]
-
         def fill(node: LoopNestNode, root_name: str) -> None:
-            perm = sched.permutation.get(root_name)
+            perm = cur.permutation.get(root_name)
             if perm is None:
                 perm = cur.default_interchange(root_name) if root_name == DEFAULT_ROOT else []
             members = set(perm)
@@ -288,9 +331,9 @@ class HipScheduler(Scheduler):
             for seg, (dim, _) in segments.items():
                 if parent_of(seg) == root_name:
                     node.splits.setdefault(dim, {})[basename(seg)] = cur.splits[dim][seg]
-            node.vectorize = [basename(v) for v in sched.vectorization if v in members]
-            node.parallelize = [basename(v) for v in sched.parallelization if v in members]
-            node.unroll = {basename(k): v for k, v in sched.unrolling.items() if k in members}
+            node.vectorize = [basename(v) for v in cur.vectorization if v in members]
+            node.parallelize = [basename(v) for v in cur.parallelization if v in members]
+            node.unroll = {basename(k): v for k, v in cur.unrolling.items() if k in members}
             node.buffer_at = {basename(k): v for k, v in cur.buffer_at.items() if k in members}
             node.pack_at = {basename(k): v for k, v in cur.pack_at.items() if k in members}
             for seg, (dim, origin) in segments.items():

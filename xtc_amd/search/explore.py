@@ -180,7 +180,7 @@ def hip_sample_filter(graph: Any, strategy_factory: Callable[..., Any]) -> Calla
     """Predicate: does this sample's schedule map exactly onto a compiled
     kernel instance?  Builds the schedule on a scratch HipBackend."""
     from ..backends.hip import Backend
-    from ..backends.hip.mapping import map_gemm
+    from ..backends.hip.mapping import map_node
     from ..backends.hip.scheduler import ScheduleError
 
     backend = Backend(graph)
@@ -196,7 +196,7 @@ def hip_sample_filter(graph: Any, strategy_factory: Callable[..., Any]) -> Calla
                 schedule = sch.schedule()
                 for ln in backend.plan.launches:
                     if ln.kind in ("matmul", "conv2d"):
-                        map_gemm(ln.attrs, ln.kind == "conv2d", schedule.node(ln.node), "strict")
+                        map_node(ln.attrs, ln.kind == "conv2d", schedule.node(ln.node), "strict")
                 cache[key] = True
             except (ScheduleError, ValueError):
                 cache[key] = False
