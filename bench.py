@@ -55,18 +55,33 @@ def _traffic(cfg: str) -> float | None:
     return None
 
 
-def _vendor_matmul(host_in: list[np.ndarray], dtype: str, steps: int, warmup: int) -> dict:
+def _warm(step, synchronize, warmup: int, warmup_ms: float) -> dict:
+    """`warmup` untimed steps, then more until `warmup_ms` of wall time has
+    passed since the first: the GPU's clocks ramp up over the first tens of
+    milliseconds of work (a cold C5 step runs 10 % slower), and the timed
+    steps measure the steady state.  Returns what ran."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < warmup_ms:
+        step()
+        n += 1
+        if n % 64 == 0 or n == warmup:
+            synchronize()  # the wall clock above measures work done, not work queued
+    synchronize()
+    return {"steps": n, "ms": round((time.perf_counter() - t0) * 1e3, 1)}
+
+
+def _vendor_matmul(host_in: list[np.ndarray], dtype: str, steps: int, warmup: int, warmup_ms: float) -> dict:
     """Times torch.matmul (hipBLASLt on this image) on the same inputs as a
-    reference point for the vendor library; bf16 inputs give a bf16 output
-    there (half the output bytes of the fp32 output measured here)."""
+    reference point for the vendor library, after the same warm-up as the
+    bench's own steps; bf16 inputs give a bf16 output there (half the output
+    bytes of the fp32 output measured here)."""
     import torch
 
     tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float32
     a = torch.from_numpy(host_in[0]).to("cuda:0").to(tdt).contiguous()
     b = torch.from_numpy(host_in[1]).to("cuda:0").to(tdt).contiguous()
-    for _ in range(warmup):
-        torch.matmul(a, b)
-    torch.cuda.synchronize()
+    _warm(lambda: torch.matmul(a, b), torch.cuda.synchronize, warmup, warmup_ms)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -260,6 +275,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup-ms", type=float, default=300.0,
+                    help="after the --warmup steps, keep stepping (untimed) until this much wall time has passed, "
+                         "so that the timed steps run at steady clocks (0: --warmup steps only)")
     ap.add_argument("--config", default="C3a", choices=["C1", "C2", "C3a", "C3b", "C4", "C5"])
     ap.add_argument("--no-protocol", action="store_true",
                     help="skip the evaluate_perf protocol pass (kernel traces then hold only the timed steps)")
@@ -333,10 +351,9 @@ def main(argv: list[str] | None = None) -> int:
         if not spot_err <= tol:
             raise SystemExit(f"parity spot check failed: scaled error {spot_err} > {tol}")
 
-    print(f"[bench] {cfg}: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        step()
-    capi.check(L.xtc_hip_synchronize(), "synchronize")
+    print(f"[bench] {cfg}: {args.warmup} warmup (at least {args.warmup_ms:g} ms) + {args.steps} timed steps",
+          file=sys.stderr, flush=True)
+    warmed = _warm(step, lambda: capi.check(L.xtc_hip_synchronize(), "synchronize"), args.warmup, args.warmup_ms)
     e0, e1 = L.xtc_hip_event_create(), L.xtc_hip_event_create()
     capi.check(L.xtc_hip_event_record(e0, None), "event")
     t0 = time.perf_counter()
@@ -383,6 +400,7 @@ def main(argv: list[str] | None = None) -> int:
             "kernel_ms": round(kernel_s * 1e3, 4),
             "pct_of_peak": round(100 * roof["frac"], 2),
             "parity_spot_scaled_err": spot_err,
+            "warmup_run": warmed,
         },
         "roofline": roof,
     }
@@ -406,7 +424,7 @@ def main(argv: list[str] | None = None) -> int:
             "kernel_frac_of_random_ceiling": round(roof["achieved"] / ceil["random"], 4),
         }
     if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
-        line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup)
+        line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup, args.warmup_ms)
     if not args.no_cpu:
         print(f"[bench] {cfg}: cpu baseline", file=sys.stderr, flush=True)
         try:
