@@ -130,11 +130,19 @@ def _cpu_baseline(cfg: str) -> dict:
         how = (f"fixed variant (i1, k1, j1)={cb.variants()[variant]}, faster at {tune}^3 than the best of {tried} "
                f"seeded tile_oo samples {sched}")
     harness = "reference evaluate_perf" if cb.ref_runtime() is not None else "evaluate_perf protocol (Python)"
+    value = 2 * m * n * k / t / 1e12
+    # the host's peak as the reference's explorer takes it: evaluate_flops's
+    # single-core FMA/s (evaluate_flops.c:461-494) times the cores
+    # (explore.py:619-625 divides the peak time by the threads)
+    fma = cb.ref_peak_flops("float32")
+    peak = {"peak_tflops": round(2 * fma * cores / 1e12, 3), "frac_of_peak": round(value / (2 * fma * cores / 1e12), 4),
+            "peak_source": "reference evaluate_flops (float32) single-core FMA/s x cores"} if fma else {}
     return {
-        "value": round(2 * m * n * k / t / 1e12, 4),
+        "value": round(value, 4),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
+        **peak,
         "sample": (
             f"fp32 matmul {m}x{n}x{k} ({'the workload shape' if cfg in ('C1', 'C2', 'C3a', 'C3b') else 'a sample'}"
             f"{', bf16-rounded inputs' if bf16 else ''}), XTC llvmir restatement in loop order i,k,j,i1,k1,j1, "

@@ -898,6 +898,13 @@ def test_direct_conv_8x14_ragged(shape):
     got = run_conv(x, w, pads=(pad, pad, pad, pad), pad_value=0.25, tile=(112, 64, 16, 1, 4))
     xp = ref.pad(x, [(0, 0), (pad, pad), (pad, pad), (0, 0)], 0.25)
     assert ref.scaled_error(got, ref.conv2d(xp, w), r * s * c, np.abs(xp).max(), 1.0) <= TOL_F32
+    # integer inputs: exact, every weight tap of the register ring and every
+    # channel chunk (the halo reload between chunks) included
+    xi = ref.np_init((n, h, wd, c), "float32") % 5
+    wi = ref.np_init((r, s, c, f), "float32") % 3 - 1
+    got = run_conv(xi, wi, pads=(pad, pad, pad, pad), pad_value=2.0, tile=(112, 64, 16, 1, 4))
+    xpi = ref.pad(xi, [(0, 0), (pad, pad), (pad, pad), (0, 0)], 2.0)
+    np.testing.assert_array_equal(got, ref.conv2d(xpi, wi).astype(np.float32))
 
 
 def test_direct_only_conv_tile_rejects_other_shapes():
