@@ -421,6 +421,20 @@ def test_split_transposed_operands_offset_the_other_way():
     assert re.search(r"= \{XTC_HIP_F32, 192, 32, 128, 256, 128, 256, ", body)
 
 
+def test_nested_split_of_the_same_axis_keeps_both_levels():
+    # i split at the root, then again inside the second segment (cut points
+    # relative to the segment): three row pieces, none lost
+    from xtc_amd.backends.hip.mapping import map_node
+
+    b = Backend(_matmul(512, 128, 256))
+    sch = b.get_scheduler()
+    sch.split("i", {"lo": 0, "hi": 128})
+    sch.split("i", {"a": 0, "b": 256}, root="./hi")
+    (ln,) = b.plan.launches
+    cfg = map_node(ln.attrs, False, sch.schedule().node(ln.node))
+    assert [(p.m0, p.M, p.n0, p.N) for p in cfg.pieces] == [(0, 128, 0, 128), (128, 256, 0, 128), (384, 128, 0, 128)]
+
+
 def test_split_on_k_or_conv_is_rejected():
     from xtc_amd.backends.hip.mapping import map_node
 

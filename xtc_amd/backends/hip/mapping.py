@@ -36,8 +36,10 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
   * split(i or j, segments) of a matmul -> one launch per segment on the
     strided sub-view of A (rows) or B (columns), C and bias, each mapped from
     its own root's tiles and knobs (src/xtc/itf/schd/scheduler.py:65-81); a
-    split on the reduction axis, or on a conv2d, is rejected: the kernels
-    overwrite C rather than accumulate into it.
+    split made inside a segment cuts that segment, its cut points counted
+    from the segment's start; a split on the reduction axis, or on a
+    conv2d, is rejected: the kernels overwrite C rather than accumulate
+    into it.
 
 Tile semantics follow the reference: a tile size is the extent of the
 sub-loop (src/xtc/backends/mlir/MlirCompilerPasses.py:414-457).

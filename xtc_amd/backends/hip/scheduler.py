@@ -98,7 +98,8 @@ class _NodeScheduler:
         self.node_name = node_name
         self.dims = list(dims)
         self.sizes = dict(sizes)
-        self.splits: dict[str, dict[str, int]] = {}
+        # (root, dim) -> qualified segment name -> start
+        self.splits: dict[tuple[str, str], dict[str, int]] = {}
         self.tiles: dict[str, dict[str, int]] = {d: {} for d in self.dims}
         self.permutation: dict[str, list[str]] = {}
         self.vectorization: list[str] = []
@@ -144,7 +145,7 @@ class _NodeScheduler:
         def rerooted(name: str) -> str:
             return loop_name(DEFAULT_ROOT, basename(name))
 
-        splits = {d: v for d, v in self.splits.items() if v and all(under(seg) for seg in v)}
+        splits = {d: v for (r, d), v in self.splits.items() if r == root and v}
         segments: list[HipSegment] = []
         for dim, segs in splits.items():
             names = list(segs)
@@ -232,7 +233,7 @@ class HipScheduler(Scheduler):
         cur = self._current
         cur._dim_of(dim)
         renamed = {loop_name(root, k): int(v) for k, v in segments.items()}
-        cur.splits[dim] = renamed
+        cur.splits[(root, dim)] = renamed
         for seg in renamed:
             cur.tiles.setdefault(seg, {})
 
@@ -310,7 +311,7 @@ class HipScheduler(Scheduler):
         nest = LoopNest(abstract_dims=list(sched.dims))
         root = nest.build_root_node(DEFAULT_ROOT)
         segments: dict[str, tuple[str, SplitOrigin]] = {}  # qualified segment -> (dim, origin)
-        for dim, segs in cur.splits.items():
+        for (_, dim), segs in cur.splits.items():
             names = list(segs)
             for idx, seg in enumerate(names):
                 end = segs[names[idx + 1]] if idx + 1 < len(names) else None
@@ -330,7 +331,7 @@ class HipScheduler(Scheduler):
                         node.tiles.setdefault(dim, {})[basename(name)] = size
             for seg, (dim, _) in segments.items():
                 if parent_of(seg) == root_name:
-                    node.splits.setdefault(dim, {})[basename(seg)] = cur.splits[dim][seg]
+                    node.splits.setdefault(dim, {})[basename(seg)] = cur.splits[(parent_of(seg), dim)][seg]
             node.vectorize = [basename(v) for v in cur.vectorization if v in members]
             node.parallelize = [basename(v) for v in cur.parallelization if v in members]
             node.unroll = {basename(k): v for k, v in cur.unrolling.items() if k in members}

@@ -1076,13 +1076,10 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
   void* dst = x.stage(slot, bytes);
   if (!dst) return nullptr;
   const int vec = 16 / elem_bytes;
-  if (R % vec == 0 && Cc % vec == 0 && ld_src % vec == 0 && aligned16(src) && aligned16(dst)) {
-    const int tile = elem_bytes == 4 ? kTransposeTileF32 : kTransposeTileBf16;
-    dim3 grid((unsigned)((Cc + tile - 1) / tile), (unsigned)((R + tile - 1) / tile));
-    if (grid.y > 65535u) {
-      fail("transpose: %d rows exceed the grid limit", R);
-      return nullptr;
-    }
+  const int vtile = elem_bytes == 4 ? kTransposeTileF32 : kTransposeTileBf16;
+  if (R % vec == 0 && Cc % vec == 0 && ld_src % vec == 0 && aligned16(src) && aligned16(dst) &&
+      (R + vtile - 1) / vtile <= 65535) {
+    dim3 grid((unsigned)((Cc + vtile - 1) / vtile), (unsigned)((R + vtile - 1) / vtile));
     if (elem_bytes == 4)
       hipLaunchKernelGGL((transpose_vec_kernel<float, kTransposeTileF32>), grid, dim3(256), 0, s, (const float*)src,
                          (float*)dst, R, Cc, ld_src);
