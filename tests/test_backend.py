@@ -435,6 +435,16 @@ def test_nested_split_of_the_same_axis_keeps_both_levels():
     assert [(p.m0, p.M, p.n0, p.N) for p in cfg.pieces] == [(0, 128, 0, 128), (128, 256, 0, 128), (384, 128, 0, 128)]
 
 
+def test_reference_explorer_compile_kwargs(tmp_path):
+    # src/xtc/search/explore.py:365-391 passes bare_ptr=False by default; the
+    # payload still takes bare device pointers, as the MLIR compiler forces
+    b = Backend(_matmul(64, 64, 64))
+    module = b.get_compiler(shared_lib=True, dump_file=str(tmp_path / "payload_0"), bare_ptr=False,
+                            debug=False).compile(b.get_scheduler().schedule())
+    assert module.file_name.endswith(".so") and Path(module.file_name).exists()
+    assert module._bare_ptr
+
+
 def test_split_on_k_or_conv_is_rejected():
     from xtc_amd.backends.hip.mapping import map_node
 
