@@ -445,6 +445,20 @@ def test_reference_explorer_compile_kwargs(tmp_path):
     assert module._bare_ptr
 
 
+def test_split_inside_a_tile_is_rejected():
+    """A split after tiles of the same axis cuts every tile: no sub-matrix
+    per segment, so no HIP mapping."""
+    from xtc_amd.backends.hip.mapping import map_node
+
+    b = Backend(_matmul(256, 256, 256))
+    sch = b.get_scheduler()
+    sch.tile("i", {"i1": 64})
+    sch.split("i", {"i_lo": 0, "i_hi": 32})
+    (ln,) = b.plan.launches
+    with pytest.raises(ScheduleError, match="inside its tiles"):
+        map_node(ln.attrs, False, sch.schedule().node(ln.node))
+
+
 def test_split_on_k_or_conv_is_rejected():
     from xtc_amd.backends.hip.mapping import map_node
 

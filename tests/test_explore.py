@@ -312,3 +312,99 @@ def test_explorer_refuses_gpu_hardware_counters(tmp_path):
         check_explore_counters(["gpu.time", "gpu.SQ_WAVES"])
     assert main(["--pmu-counters", "gpu.cycles", "--output", str(tmp_path / "x.csv")]) == 2
     assert not (tmp_path / "x.csv").exists()
+
+
+# ---------------------------------------------------------------- the reference's remaining CLI flags
+
+def test_cli_listing_flags(capsys):
+    from xtc_amd.cli.explore import main
+
+    assert main(["--operator-list"]) == 0
+    assert capsys.readouterr().out.split() == ["matmul", "conv2d", "relu"]
+    assert main(["--strategy-list"]) == 0
+    assert "tile_hip" in capsys.readouterr().out.split()
+    assert main(["--operator", "conv2d", "--op-name-list"]) == 0
+    out = capsys.readouterr().out.splitlines()
+    # src/xtc/artifacts: 32 layers of Yolo9000/MobileNet/ResNet18, then 17 of SqueezeNet/AlexNet
+    assert len(out) == 49 and out[0].startswith("Yolo9000_00: {'n': 1, 'h': 544")
+    assert "ResNet18_04: {'n': 1, 'h': 56, 'w': 56, 'f': 128, 'r': 3, 's': 3, 'c': 64}, {'SH': 2, 'SW': 2}" in out
+
+
+def test_named_operations_follow_the_reference_registry():
+    from xtc_amd.artifacts import get_operation, has_operation, list_operations
+    from xtc_amd.cli.explore import _operation_dims
+
+    assert _operation_dims("conv2d", "resnet18_04") == [1, 56, 56, 128, 3, 3, 64, 2, 2]
+    assert _operation_dims("matmul", "Gemma9B_FC") == [3584, 14336, 3584]
+    assert get_operation("matmul", "AlexNet_FC6")["dims"] == {"i": 1, "j": 4096, "k": 9216}
+    assert len(list_operations("matmul")) == 27 and has_operation("conv2d", "SQUEEZENET_21")
+    with pytest.raises(ValueError, match="not registered"):
+        get_operation("matmul", "ResNet18_04")
+    g = build_graph("conv2d", _operation_dims("conv2d", "ResNet18_01"), "float32", name="rn18_01")
+    assert g.name == "rn18_01"
+    assert [str(t) for t in g.inputs_types] == ["1x454x454x3xfloat32", "7x7x3x64xfloat32"]
+
+
+def test_cli_rejects_resume_with_append(tmp_path):
+    from xtc_amd.cli.explore import main
+
+    with pytest.raises(SystemExit):
+        main(["--resume", "--append", "--output", str(tmp_path / "x.csv")])
+
+
+def test_cli_compile_only_runs_record_nothing(tmp_path, capsys):
+    """--no-execute compiles each sample (payload libraries under
+    --explore-dir, sources under --save-temps-dir) and evaluates none; the
+    CSV keeps its header only."""
+    from xtc_amd.cli.explore import main
+
+    out = tmp_path / "r.csv"
+    temps = tmp_path / "temps"
+    rc = main(["--operator", "matmul", "--dims", "256", "256", "256", "--trials", "3", "--no-execute", "--quiet",
+               "--output", str(out), "--explore-dir", str(tmp_path), "--save-temps", "--save-temps-dir", str(temps),
+               "--func-name", "mm256", "--jobs", "2"])
+    assert rc == 0
+    assert len(list(csv.DictReader(open(out)))) == 0
+    assert (temps / "mm256.graph.yaml").exists()
+    assert sorted(p.name for p in temps.iterdir() if p.is_dir()) == ["0000", "0001", "0002"]
+    assert capsys.readouterr().out == ""
+
+
+def test_cli_opt_level_and_test_evaluate_one_schedule(tmp_path, monkeypatch, capsys):
+    from xtc_amd.cli.explore import main
+
+    seen = []
+
+    def evaluate_one(self, module):
+        seen.append(module)
+        return [1e-3], 0, ""
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    # the reference evaluates the default schedule at --opt-level 0-3
+    assert main(["--operator", "matmul", "--dims", "256", "256", "256", "--opt-level", "2", "--peak-flops", "1e12",
+                 "--output", str(tmp_path / "a.csv")]) == 0
+    assert len(seen) == 1
+    assert capsys.readouterr().out.startswith("Schedule: hip: [")
+    g = build_graph("matmul", [256, 256, 256], "float32")
+    x = Strategies.create("tile_hip", g).default_schedule(2)
+    assert main(["--operator", "matmul", "--dims", "256", "256", "256", "--test", *map(str, x), "--quiet", "--peak-flops", "1e12",
+                 "--output", str(tmp_path / "b.csv")]) == 0
+    rows = list(csv.DictReader(open(tmp_path / "b.csv")))
+    assert len(seen) == 2 and len(rows) == 1 and parse_x(rows[0]["X"]) == list(x)
+
+
+def test_cli_descript_spec_replaces_the_strategy(tmp_path, monkeypatch):
+    """--descript: the spec's parameters are the CSV columns, and every
+    sample kept by the HIP filter compiles to a kernel instance."""
+    from xtc_amd.cli.explore import main
+
+    monkeypatch.setattr(Exploration, "evaluate_one", lambda self, module: ([1e-3], 0, ""))
+    spec = tmp_path / "spec.yaml"
+    spec.write_text("i:\nj:\nk:\ni#bm:\nj#bn:\nk#bk:\ni#wm:\nj#wn:\n")
+    out = tmp_path / "d.csv"
+    assert main(["--operator", "matmul", "--dims", "512", "512", "512", "--descript", str(spec), "--trials", "4", "--peak-flops", "1e12",
+                 "--quiet", "--output", str(out), "--db-file", str(tmp_path / "d.jsonl"), "--jobs", "2"]) == 0
+    rows = list(csv.DictReader(open(out)))
+    assert list(rows[0])[:5] == ["bm", "bn", "bk", "wm", "wn"] and len(rows) == 4
+    db = [json.loads(l) for l in open(tmp_path / "d.jsonl")]
+    assert all(d["strategy"][2] == "descript" and d["kernels"]["C"].startswith("gemm<float32>") for d in db)

@@ -50,4 +50,17 @@ def test_loop_explore_c1_iterative(tmp_path):
                                 "random-forest-default")
     assert len(recs) == 6 and all(r["results"][0] == 0 for r in recs), [r["error"] for r in recs]
     assert 1 <= len(rows) <= 6
-    assert "best" in proc.stdout
+    # the reference's closing line: best schedule, time and fraction of peak
+    assert "Schedule: hip: [" in proc.stdout and "peak perf:" in proc.stdout
+
+
+def test_loop_explore_descript_spec_validated(tmp_path):
+    """--descript: a spec's free tile sizes, sampled under the HIP filter,
+    compiled, run and validated on the device."""
+    spec = tmp_path / "spec.yaml"
+    spec.write_text("i: parallelize\nj: parallelize\nk:\ni#bm:\nj#bn:\nk#bk:\ni#wm:\nj#wn:\n")
+    rows, recs, proc = _explore(tmp_path, "--descript", str(spec), "--trials", "6", "--validate")
+    assert len(recs) == 6 and all(r["results"][0] == 0 for r in recs), [r["error"] for r in recs]
+    assert len(rows) == 6 and list(rows[0])[:5] == ["bm", "bn", "bk", "wm", "wn"]
+    assert all(r["strategy"][2] == "descript" for r in recs)
+    assert all(1.7e-6 < float(r["time"]) < 1e-3 for r in rows)

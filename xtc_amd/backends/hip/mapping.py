@@ -376,6 +376,11 @@ def _split_pieces(attrs: dict[str, Any], conv: bool, sched: HipNodeSchedule, pol
     if dim == k_dim:
         raise ScheduleError(f"{where} on the reduction axis {dim!r} has no HIP mapping: the kernels overwrite C "
                             "rather than accumulate into it")
+    if sched.levels(dim):
+        # the split then cuts every tile of the axis, so each segment is a
+        # strided set of rows or columns rather than one sub-matrix
+        raise ScheduleError(f"{where} of {dim!r} inside its tiles ({sched.levels(dim)}) has no HIP mapping: only a "
+                            "split of the untiled axis becomes one launch per segment")
     extent = attrs["M"] if dim == m_dim else attrs["N"]
     segs = list(sched.segments)
     if segs[0].start != 0:

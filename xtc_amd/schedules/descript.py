@@ -22,7 +22,9 @@ HIP backend then maps the resulting tiles onto kernel template parameters.
 
 from __future__ import annotations
 
+import ast
 import copy
+import functools
 import re
 from dataclasses import dataclass, field
 from typing import Any
@@ -306,6 +308,19 @@ class ScheduleInterpreter:
                 if name:
                     loop = name
                 self._annotate(item.annotations, loop, sizes, node, constraints)
+        # a segment of variable size that ends the axis ends at its extent:
+        # its cut placeholder is replaced by that extent
+        for name, total in sized_cuts:
+            axis = next((a for a, c in cut.items() if c == name), None)
+            if axis is None or total is None:
+                continue
+            word = re.compile(rf"\b{re.escape(name)}\b")
+            constraints[:] = [word.sub(str(total), c) for c in constraints]
+            for child in node.children:
+                origin = child.split_origin
+                if origin is not None and origin.end == name:
+                    child.split_origin = SplitOrigin(axis=origin.axis, start=origin.start, end=total)
+            cut[axis] = total
         for axis, c in cut.items():
             full = extents[axis][-1] if extents.get(axis) else None
             if isinstance(c, int) and c not in (0, full):
@@ -348,8 +363,15 @@ class ScheduleInterpreter:
             if isinstance(item.size, int) and isinstance(prev, int):
                 cut[axis] = prev + item.size
                 seg_end = prev + item.size
+            elif prev == 0:
+                cut[axis] = item.size
+                seg_end = item.size
             else:
                 new_cut = (root.lstrip(".").lstrip("/") + name).replace("[", "_").replace("]", "_").replace("/", "")
+                if sized_cuts:
+                    # an earlier variable cut lies within the extent
+                    constraints.append(f"{sized_cuts[-1][0]} <= {sized_cuts[-1][1]}")
+                sized_cuts.append((new_cut, total))
                 cut[axis] = new_cut
                 constraints.append(f"{item.size} + {prev} == {new_cut}")
                 seg_end = new_cut
@@ -451,48 +473,67 @@ class ScheduleInterpreter:
 # ------------------------------------------------------------------ parameters
 
 
+_EXPR_NODES = (ast.Expression, ast.BinOp, ast.UnaryOp, ast.Add, ast.Sub, ast.Mult, ast.FloorDiv, ast.USub,
+               ast.UAdd, ast.Constant, ast.Name, ast.Load)
+_COMPARE_NODES = (ast.Compare, ast.LtE, ast.GtE, ast.Lt, ast.Gt, ast.Eq, ast.NotEq)
+
+
+@functools.lru_cache(maxsize=4096)
+def compile_expr(text: str, compare: bool = False) -> tuple[Any, tuple[str, ...]]:
+    """An integer expression over parameters (+, -, *, //, parentheses), or
+    with `compare` a chain of comparisons of such expressions, as
+    (code object, parameter names).  Anything else is refused."""
+    try:
+        tree = ast.parse(text.strip(), mode="eval")
+    except SyntaxError as err:
+        raise ScheduleValidationError(f"cannot parse `{text}`: {err.msg}") from None
+    allowed = _EXPR_NODES + (_COMPARE_NODES if compare else ())
+    for n in ast.walk(tree):
+        if not isinstance(n, allowed) or (isinstance(n, ast.Constant) and type(n.value) is not int):
+            raise ScheduleValidationError(f"unsupported expression `{text}`")
+    if compare and not isinstance(tree.body, ast.Compare):
+        raise ScheduleValidationError(f"unsupported constraint `{text}`")
+    names = tuple(dict.fromkeys(n.id for n in ast.walk(tree) if isinstance(n, ast.Name)))
+    return compile(tree, "<descript>", "eval"), names
+
+
+def _eval(text: str, sample: dict[str, int], compare: bool = False) -> int:
+    code, names = compile_expr(text, compare)
+    env = {}
+    for n in names:
+        if n not in sample:
+            raise ScheduleValidationError(f"parameter {n} has no value in the sample")
+        env[n] = int(sample[n])
+    return eval(code, {"__builtins__": {}}, env)  # noqa: S307 - whitelisted integer AST
+
+
 def _value(token: str, sample: dict[str, int]) -> int:
-    token = token.strip()
-    if token.lstrip("-").isdigit():
-        return int(token)
-    if token in sample:
-        return int(sample[token])
-    raise ScheduleValidationError(f"parameter {token} has no value in the sample")
+    return int(_eval(token, sample))
 
 
 def _expr(text: str, sample: dict[str, int]) -> int:
-    """Sums and differences of integers and parameters."""
-    total, sign, tok = 0, 1, ""
-    for ch in text.replace(" ", "") + "+":
-        if ch in "+-" and tok:
-            total += sign * _value(tok, sample)
-            sign, tok = (1 if ch == "+" else -1), ""
-        else:
-            tok += ch
-    return total
+    return int(_eval(text, sample))
+
+
+def _members(text: str) -> list[str]:
+    return [v for v in text.strip().strip("{}").split(",") if v.strip()]
 
 
 def check_constraints(constraints: list[str], sample: dict[str, int]) -> None:
-    """Evaluates the constraint forms the interpreter emits:
-    `a <= b`, `a == b`, `a in {x, y}`, and `a || {b, c}` / `a || b`
-    (a divides every listed size)."""
+    """Evaluates the constraint forms of descript specs and their
+    interpreter: comparisons of integer expressions (`a <= b`,
+    `a * b >= 8`, `a == b + c`, ...), `a in {x, y}`, and `a || {b, c}` /
+    `a || b` (a divides every listed size)."""
     for c in constraints:
         if " in " in c:
             lhs, rhs = c.split(" in ", 1)
-            allowed = {_expr(v, sample) for v in rhs.strip().strip("{}").split(",") if v.strip()}
-            ok = _expr(lhs, sample) in allowed
+            ok = _expr(lhs, sample) in {_expr(v, sample) for v in _members(rhs)}
         elif "||" in c:
             lhs, rhs = c.split("||", 1)
             a = _expr(lhs, sample)
-            ok = a > 0 and all(_expr(v, sample) % a == 0 for v in rhs.strip().strip("{}").split(",") if v.strip())
-        elif "<=" in c:
-            lhs, rhs = c.split("<=", 1)
-            ok = _expr(lhs, sample) <= _expr(rhs, sample)
-        elif "==" in c:
-            lhs, rhs = c.split("==", 1)
-            ok = _expr(lhs, sample) == _expr(rhs, sample)
+            ok = a > 0 and all(_expr(v, sample) % a == 0 for v in _members(rhs))
         else:
-            raise ScheduleValidationError(f"unsupported constraint `{c}`")
+            ok = bool(_eval(c, sample, compare=True))
         if not ok:
             raise ScheduleValidationError(f"constraint `{c}` does not hold for {sample}")
 

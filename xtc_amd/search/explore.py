@@ -76,6 +76,14 @@ class ExplorationConfig:
     append: bool = False
     peak_flops: float | None = None  # FMA/s; default: the device's dense MFMA peak
     compile_kwargs: dict[str, Any] = field(default_factory=dict)
+    test: list[int] = field(default_factory=list)  # evaluate this one sample only
+    execute: bool = True  # False: compile every sample, evaluate none
+    quiet: bool = False  # no per-sample lines
+    dump: bool = False  # print every payload's generated C source
+    save_temps: bool = False  # keep payload sources under save_temps_dir/<ident>
+    save_temps_dir: str = "./save_temps_dir"
+    explore_dir: str | None = None  # where the payload libraries go (dump_file = <dir>/payload_<ident>)
+    descript: str | None = None  # path to a descript YAML spec; replaces `strategy` when set
 
 
 class CSVCallback:
@@ -231,16 +239,30 @@ class Exploration:
         self.graph = graph
         self.config = config
         self._backend_mod = import_module(f"xtc_amd.backends.{config.backend}")
+        factory = self._strategy_factory(graph, config)
         kwargs = dict(config.strategy_kwargs)
-        if config.backend == "hip" and Strategies.resolve_name(config.strategy) != "tile_hip":
-            kwargs["sample_filter"] = hip_sample_filter(
-                graph, lambda: Strategies.create(config.strategy, graph, **config.strategy_kwargs)
-            )
-        self.strategy = Strategies.create(config.strategy, graph, **kwargs)
+        if config.backend == "hip" and (config.descript or Strategies.resolve_name(config.strategy) != "tile_hip"):
+            kwargs["sample_filter"] = hip_sample_filter(graph, factory)
+        self.strategy = factory(**kwargs)
+        self.peak_time_s = 0.0  # the graph's time at peak, set by run()
+
+    @staticmethod
+    def _strategy_factory(graph: Any, config: ExplorationConfig) -> Callable[..., Any]:
+        """Strategy constructor: a descript spec file replaces the named
+        strategy (src/xtc/search/explore.py:817-834)."""
+        if config.descript:
+            from .descript_strategy import Strategy_Descript
+
+            with open(config.descript) as f:
+                spec = f.read()
+            return lambda **kw: Strategy_Descript(graph, spec, **{**config.strategy_kwargs, **kw})
+        return lambda **kw: Strategies.create(config.strategy, graph, **{**config.strategy_kwargs, **kw})
 
     # ---- sample sources
     def samples(self) -> list[list[int]]:
         c = self.config
+        if c.test:
+            return [list(c.test)]
         if c.search == "exhaustive":
             from itertools import islice
 
@@ -257,12 +279,20 @@ class Exploration:
         raise ValueError(f"unknown search {c.search!r}")
 
     # ---- one sample
-    def compile_one(self, sample: list[int]) -> Any:
+    def compile_one(self, sample: list[int], ident: str = "0000") -> Any:
+        c = self.config
         backend = self._backend_mod.Backend(self.graph)
         sch = backend.get_scheduler()
         self.strategy.generate(sch, sample)
-        kwargs = {"shared_lib": True, **self.config.compile_kwargs}
-        if self.config.backend == "hip":
+        kwargs = {"shared_lib": True, **c.compile_kwargs}
+        if c.explore_dir:
+            kwargs.setdefault("dump_file", f"{c.explore_dir}/payload_{ident}")
+        if c.dump:
+            kwargs.setdefault("print_source_ir", True)
+        if c.save_temps:
+            kwargs.setdefault("save_temps", True)
+            kwargs.setdefault("save_temps_dir", f"{c.save_temps_dir}/{ident}")
+        if c.backend == "hip":
             kwargs.setdefault("schedule_policy", "strict")
         return backend.get_compiler(**kwargs).compile(sch.schedule())
 
@@ -323,6 +353,14 @@ class Exploration:
     ) -> tuple[list[int], list[float], int, str]:
         c = self.config
         extra: dict[str, Any] = {}
+        if not c.execute:
+            # compile only: a compile error is reported, nothing is timed or recorded
+            try:
+                fut.result()
+                return (sample, [], 0, "compiled, not executed")
+            except Exception as err:
+                logger.warning("sample %s failed to compile: %s", sample, err)
+                return (sample, [], 2, f"{type(err).__name__}: {err}")
         try:
             module = fut.result()
             extra = {"kernels": {k: v.describe() for k, v in getattr(module, "configs", {}).items()}, "error": ""}
@@ -343,13 +381,14 @@ class Exploration:
         self, pool: cf.ThreadPoolExecutor, todo: list[list[int]], csv_cb: CSVCallback, db_cb: DBCallback | None,
         done: int, total: int,
     ) -> list[tuple[list[int], list[float], int, str]]:
-        futures = [pool.submit(self.compile_one, s) for s in todo]
+        futures = [pool.submit(self.compile_one, s, f"{done + i:04}") for i, s in enumerate(todo)]
         out = []
         for idx, (sample, fut) in enumerate(zip(todo, futures)):
             res = self._evaluate_compiled(sample, fut, csv_cb, db_cb)
             out.append(res)
             best = min(res[1]) if res[1] else 0.0
-            logger.info("[%d/%d] %s -> %.3g s (%s)", done + idx + 1, total, sample, best, res[3] or "ok")
+            if not self.config.quiet:
+                logger.info("[%d/%d] %s -> %.3g s (%s)", done + idx + 1, total, sample, best, res[3] or "ok")
         return out
 
     def run(self) -> list[tuple[list[int], list[float], int, str]]:
@@ -369,9 +408,14 @@ class Exploration:
                 samples: list[list[int]] = []
             else:
                 samples = self.samples()
-            peak_time = self.peak_time()
+            # compile-only runs never touch the GPU
+            peak_time = self.peak_time() if c.execute else 0.0
+            self.peak_time_s = peak_time
+            if c.save_temps:
+                Path(c.save_temps_dir).mkdir(parents=True, exist_ok=True)
+                self.graph.dump(str(Path(c.save_temps_dir) / f"{self.graph.name}.graph.yaml"))
             csv_cb = CSVCallback(c.output, peak_time, self.strategy.sample_names, resume=c.resume, append=c.append)
-            db_cb = DBCallback(c.db_file, self.graph, c.strategy) if c.db_file else None
+            db_cb = DBCallback(c.db_file, self.graph, "descript" if c.descript else c.strategy) if c.db_file else None
             try:
                 with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
                     if c.search == "iterative":
@@ -383,7 +427,8 @@ class Exploration:
                 csv_cb.close()
                 if db_cb:
                     db_cb.close()
-            logger.info("explored %d samples in %.1f s", len(results), time.time() - t0)
+            if not c.quiet:
+                logger.info("explored %d samples in %.1f s", len(results), time.time() - t0)
         return results
 
     def _run_iterative(
