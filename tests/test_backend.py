@@ -673,6 +673,20 @@ def test_instances_and_default_tile():
     assert tuple(capi.default_tile("float32", False, 2048, 2048, 2048)[0]) == (128, 128, 32, 2, 2)
     tile, split = capi.default_tile("bfloat16", False, 8192, 8192, 8192)
     assert tuple(tile) == (256, 256, 32, 2, 4) and split == 1
+    # few 64x64 tiles over a deep K: split-K up to 1024 workgroups and 32
+    # splits, >= 4 slabs per split; from 128 tiles only over K >= 512
+    cases = {
+        ("float32", True, 49, 512, 4608): ((64, 64, 16, 2, 2), 32),      # ResNet18_12: 8 tiles
+        ("float32", True, 8 * 56 * 56, 64, 576): ((64, 64, 16, 2, 2), 1),  # C4: 392 tiles, direct conv
+        ("float32", True, 68 * 68, 128, 256): ((64, 64, 16, 2, 2), 1),     # Yolo9000_09: 146 tiles, K 256
+        ("float32", True, 112 * 112, 64, 576): ((64, 64, 16, 2, 2), 4),    # MobilNet_02: 196 tiles
+        ("float32", False, 512, 512, 512): ((64, 64, 32, 2, 2), 4),        # 64 tiles, 4 slabs per split
+        ("float32", False, 128, 4096, 8192): ((64, 64, 32, 2, 2), 8),      # Llama3_QK: 128 tiles
+        ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 1),     # 1152 tiles
+    }
+    for args, (tile, split) in cases.items():
+        got = capi.default_tile(*args)
+        assert (tuple(got[0]), got[1]) == (tile, split), (args, got)
 
 
 def test_datasheet_flops_are_half_the_flop_rate():

@@ -314,6 +314,31 @@ def test_conv_unaligned_channels_fallback():
     assert ref.scaled_error(out, expect, 27, 1.0, 1.0) <= TOL_F32
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_conv_unaligned_channels_staged(dtype):
+    """C = 3 with F a multiple of the vector: the input and the weights are
+    staged with zero channels up to 4 (fp32) or 8 (bf16) and the MFMA conv
+    runs on the copies; a finite pad value times a zero weight adds 0."""
+    x = rng_uniform(21, (2, 23, 19, 3))
+    w = rng_uniform(22, (5, 3, 3, 16))
+    if dtype == "bfloat16":
+        x, w = ref.round_bf16(x), ref.round_bf16(w)
+    pads = (2, 1, 1, 2)
+    out = run_conv(x, w, dtype, stride=(2, 1), pads=pads, pad_value=0.5)
+    xp = ref.pad(x, [(0, 0), (2, 1), (1, 2), (0, 0)], 0.5)
+    expect = ref.conv2d(xp, w, (2, 1))
+    err = ref.scaled_error(out, expect, 5 * 3 * 3, 1.0, np.abs(w).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+    # integer inputs: exact, also with an explicit tile and split-K
+    xi = ref.np_init((1, 17, 17, 3), "float32")
+    wi = (ref.np_init((7, 7, 3, 32), "float32") - 5.0).copy()
+    expect = ref.conv2d(ref.pad(xi, [(0, 0), (3, 3), (3, 3), (0, 0)]), wi, (2, 2)).astype(np.float32)
+    tile = (64, 64, 16, 2, 2) if dtype == "float32" else (64, 64, 32, 2, 2)
+    for tile, split in ((None, 0), (tile, 2)):
+        out = run_conv(xi, wi, dtype, stride=(2, 2), pads=(3, 3, 3, 3), tile=tile, split_k=split)
+        np.testing.assert_array_equal(out, expect)
+
+
 # ------------------------------------------------------------- aux kernels
 
 

@@ -83,7 +83,11 @@ b = O.tensor((512, 512), "float32", name="B")
 with O.graph(name="matmul_mixed_counters") as gb:
     O.matmul(a, b, name="C")
 backend = Backend(gb.graph)
-module = backend.get_compiler().compile(backend.get_scheduler().schedule())
+sch = backend.get_scheduler()
+sch.tile("i", {{"i1": 64, "i2": 32}})
+sch.tile("j", {{"j1": 64, "j2": 32}})
+sch.tile("k", {{"k1": 16}})
+module = backend.get_compiler().compile(sch.schedule())
 # the reference GPU test's host names (tests/filecheck/evaluation/test_matmul_pmu_counters_gpu.py:34-46)
 # beside gpu.* counters, in one call
 names = ["cycles", "instructions", "clocks", "mem_load_retired.l1_miss", "context_switches", "gpu.cycles",

@@ -442,6 +442,22 @@ __global__ void conv_naive_kernel(const T* I, const T* Wt, float* O, const float
   }
 }
 
+// dst[r][c] = src[r][c] for c < C, 0 for C <= c < Cp, over `rows` rows of C
+// (src) and Cp (dst) elements: the channel padding that gives a conv input
+// (rows = N*H*W pixels) or its RSCF weights (rows = R*S taps, C*F and Cp*F
+// elements) 16-byte channel vectors.  HBM-bound copy.
+template <typename T>
+__global__ void __launch_bounds__(256) pad_channels_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                           uint64_t rows, uint32_t C, uint32_t Cp) {
+  const uint64_t total = rows * Cp;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint64_t r = i / Cp;
+    const uint32_t c = (uint32_t)(i - r * Cp);
+    dst[i] = c < C ? src[r * C + c] : T(0);
+  }
+}
+
 float bf16_round_host(float v) {
   unsigned u;
   memcpy(&u, &v, 4);
@@ -549,7 +565,28 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   };
   const bool f32 = dtype == XTC_HIP_F32;
   const int bk = f32 ? 32 : 64;
-  if (conv && f32 && N % 64 == 0 && K % 64 == 0 && pick(64, 64, 16, 2, 2)) return;
+  // Fewer 64x64 tiles than the chip has CUs (256; 512 for a matmul) over a
+  // deep K: split K, completed inside the launch, by powers of two up to
+  // 1024 workgroups and 32 splits, with at least 4 slabs per split; from
+  // 128 tiles on, only over a K of at least 512.  Measured on MI355X over
+  // the op-name layers: ResNet18_12 148 -> 24 us, MobilNet_09 314 -> 37 us,
+  // MobilNet_02 (196 tiles, K 576) 34 -> 26 us, Llama3_QK 242 -> 89 us,
+  // 512^3 fp32 19 -> 13 us; Yolo9000_09 (146 tiles, K 256) lost 7-12 % at
+  // split 2 or 4 against its direct conv, and shapes with more tiles gain
+  // little or lose (C4's 392 tiles keep the direct conv).
+  auto fill = [&](int64_t below) {
+    const int64_t tiles = (int64_t)((M + t->bm - 1) / t->bm) * ((N + t->bn - 1) / t->bn);
+    if (tiles >= below || (tiles >= 128 && K < 512)) return;
+    int s = 1;
+    while (s < 32 && tiles * s * 2 <= 1024 && K % (2 * s) == 0 && (K / (2 * s)) % t->bk == 0 &&
+           K / (2 * s) >= 4 * t->bk)
+      s *= 2;
+    *split_k = s;
+  };
+  if (conv && f32 && N % 64 == 0 && K % 64 == 0 && pick(64, 64, 16, 2, 2)) {
+    fill(256);
+    return;
+  }
   if (M <= 16) {
     // skinny bf16 with aligned N and K: the B-streaming kernel
     // (gemm_bf16_skinny.hpp) behind tile 16x128x64, 1x4 waves, 1024-deep splits
@@ -590,10 +627,10 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   if (M >= 2048 && N >= 2048) {
     if (pick(128, 128, bk, 2, 2)) return;
   }
-  if (N <= 64) {
-    if (pick(64, 64, bk, 2, 2)) return;
+  if (pick(64, 64, bk, 2, 2)) {
+    fill(conv ? 256 : 512);
+    return;
   }
-  if (pick(64, 64, bk, 2, 2)) return;
   int n = 0;
   const GemmEntry* e = gemm_registry(&n);
   for (int i = 0; i < n; ++i)
@@ -1661,6 +1698,38 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   const int M = d.N * OH * OW;
   const int K = d.R * d.S * d.C;
   const bool vec_ok = d.C % vec == 0 && d.F % vec == 0 && aligned16(input) && aligned16(weight);
+  const bool padded = d.pad_top || d.pad_bottom || d.pad_left || d.pad_right;
+  if (!vec_ok && d.F % vec == 0 && (!padded || isfinite(d.pad_value))) {
+    // Channels that are not whole 16-byte vectors (C = 3 image inputs): the
+    // input and the weights are copied with zero channels up to Cp, a
+    // multiple of the vector, and the MFMA conv runs on the copies.  A zero
+    // channel adds exact zeros (input 0 or a finite pad value, times a zero
+    // weight), so the result is the conv over the C real channels.
+    const int Cp = (d.C + vec - 1) / vec * vec;
+    const size_t esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
+    const uint64_t pixels = (uint64_t)d.N * d.H * d.W, taps = (uint64_t)d.R * d.S;
+    if ((uint64_t)Cp * d.F > 0xffffffffu) return fail("conv2d: %d x %d channels too many to stage", Cp, d.F);
+    Scratch x{s};
+    void* in_c = x.stage(0, pixels * Cp * esz);
+    void* w_c = in_c ? x.stage(1, taps * Cp * d.F * esz) : nullptr;
+    if (!in_c || !w_c) return 1;
+    if (d.dtype == XTC_HIP_F32) {
+      hipLaunchKernelGGL(pad_channels_kernel<float>, dim3(grid_for(pixels * Cp, 256)), dim3(256), 0, s,
+                         (const float*)input, (float*)in_c, pixels, (uint32_t)d.C, (uint32_t)Cp);
+      hipLaunchKernelGGL(pad_channels_kernel<float>, dim3(grid_for(taps * Cp * d.F, 256)), dim3(256), 0, s,
+                         (const float*)weight, (float*)w_c, taps, (uint32_t)(d.C * d.F), (uint32_t)(Cp * d.F));
+    } else {
+      hipLaunchKernelGGL(pad_channels_kernel<uint16_t>, dim3(grid_for(pixels * Cp, 256)), dim3(256), 0, s,
+                         (const uint16_t*)input, (uint16_t*)in_c, pixels, (uint32_t)d.C, (uint32_t)Cp);
+      hipLaunchKernelGGL(pad_channels_kernel<uint16_t>, dim3(grid_for(taps * Cp * d.F, 256)), dim3(256), 0, s,
+                         (const uint16_t*)weight, (uint16_t*)w_c, taps, (uint32_t)(d.C * d.F),
+                         (uint32_t)(Cp * d.F));
+    }
+    HIP_TRY(hipGetLastError());
+    xtc_hip_conv2d_desc dc = d;
+    dc.C = Cp;
+    return xtc_hip_conv2d(&dc, in_c, w_c, out, bias);
+  }
   if (!vec_ok) {
     dim3 grid(grid_for((uint64_t)M * d.F, 128));
     if (d.dtype == XTC_HIP_F32)

@@ -568,8 +568,10 @@ class Strategy_HIP(BaseStrategy):
         plus parallelize(k);
       * conv2d (b, h, w, f, r, s, c): the implicit-GEMM rows are b*h*w, so
         the block and wave heights are split over h and w (w takes up to 8),
-        f carries the block and wave widths and c the slab depth; split_k is 1;
-      * stages: unroll of the slab loop (k, or k1 under split-K; c for conv)
+        f carries the block and wave widths and c the slab depth, {c1: bk};
+        with split_k > 1, {c1: K/split_k, c2: bk} plus parallelize(c), for
+        the splits whose slice K/split_k is at most C;
+      * stages: unroll of the slab loop (k, or k1 under split-K; c or c1 for conv)
         by the pipeline depth, one of the depths the tile's kernel is
         compiled for on this shape (the default first).
     """
@@ -597,11 +599,15 @@ class Strategy_HIP(BaseStrategy):
         self._attrs = self._launch_attrs(graph, _node_of(graph, kwargs.get("node")).name)
         tiles = sorted(set(legal_tiles(dtype, self._conv)))
         self._tiles = [t for t in tiles if t[0] <= max(16, self._M) * 2 and t[1] <= max(16, self._N) * 2]
+        splits = (1, 2, 4, 8, 16, 32)
         if self._conv:
             self._tiles = [t for t in self._tiles if t[2] <= self._C]
-            self._splits = [1]
+            # a split's K slice is a tile of c (c1 = K / split), so it is at
+            # most C: splits of at least R*S, each slice within one tap's channels
+            self._splits = [s for s in splits
+                            if s == 1 or (self._K % s == 0 and 64 <= self._K // s <= self._C)]
         else:
-            self._splits = [s for s in (1, 2, 4, 8, 16) if s == 1 or (self._K % s == 0 and self._K // s >= 64)]
+            self._splits = [s for s in splits if s == 1 or (self._K % s == 0 and self._K // s >= 64)]
         self._dtype = dtype
 
     @staticmethod
@@ -655,10 +661,17 @@ class Strategy_HIP(BaseStrategy):
             sch.tile(h, {f"{h}1": bm // w1, f"{h}2": wm // w2})
             sch.tile(w, {f"{w}1": w1, f"{w}2": w2})
             sch.tile(f, {f"{f}1": bn, f"{f}2": wn})
-            sch.tile(c, {f"{c}1": bk})
-            sch.parallelize([b, h, w, f])
+            if split > 1:
+                # split-K: parallel slices of K / split reduction elements
+                sch.tile(c, {f"{c}1": self._K // split, f"{c}2": bk})
+                sch.parallelize([b, h, w, f, c])
+                slab = f"{c}1"
+            else:
+                sch.tile(c, {f"{c}1": bk})
+                sch.parallelize([b, h, w, f])
+                slab = c
             if depth is not None:
-                sch.unroll({c: depth})  # the slab loop: `depth` slabs in flight
+                sch.unroll({slab: depth})  # the slab loop: `depth` slabs in flight
             return
         i, j, k = self._dims
         sch.tile(i, {f"{i}1": bm, f"{i}2": wm})
@@ -687,6 +700,9 @@ class Strategy_HIP(BaseStrategy):
             tile, split = capi.default_tile(self._dtype, self._conv, self._M, self._N, self._K)
         bm, bn, bk, wgm, wgn = tile
         split = max(1, split)
+        if split not in self._splits:
+            # a library split this space cannot name (a conv slice wider than C)
+            split = max(s for s in self._splits if s <= split and (s == 1 or (self._K // s) % bk == 0))
         return [bm, bm // wgm, bn, bn // wgn, bk, split, self._depths(tile, split)[0]]
 
 
