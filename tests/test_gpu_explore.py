@@ -64,3 +64,22 @@ def test_loop_explore_descript_spec_validated(tmp_path):
     assert len(rows) == 6 and list(rows[0])[:5] == ["bm", "bn", "bk", "wm", "wn"]
     assert all(r["strategy"][2] == "descript" for r in recs)
     assert all(1.7e-6 < float(r["time"]) < 1e-3 for r in rows)
+
+
+def test_loop_explore_named_conv_with_split_k(tmp_path):
+    """--op-name picks a reference layer (ResNet18_12: 7x7 outputs, 512
+    channels, K 4608); tile_hip samples its split-K points, each validated."""
+    out = tmp_path / "n.csv"
+    cmd = [sys.executable, "-u", "-m", "xtc_amd.cli.explore", "--operator", "conv2d", "--op-name", "ResNet18_12",
+           "--strategy", "tile_hip", "--search", "exhaustive", "--trials", "40", "--validate", "--repeat", "1",
+           "--min-repeat-ms", "5", "--jobs", "4", "--quiet", "--output", str(out)]
+    print("[explore]", " ".join(cmd[3:]), flush=True)
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    rows = list(csv.DictReader(open(out)))
+    assert len(rows) >= 20 and {int(r["split_k"]) for r in rows} >= {1, 16, 32}
+    times = {int(r["split_k"]): min(float(x["time"]) for x in rows if int(x["split_k"]) == int(r["split_k"]))
+             for r in rows}
+    # splitting the 4608-deep K over 16-32 slices is several times faster
+    assert min(times[16], times[32]) * 2 < times[1]
+
