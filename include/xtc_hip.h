@@ -231,7 +231,9 @@ int xtc_hip_conv2d_default_tile(const xtc_hip_conv2d_desc *desc, xtc_hip_tile *o
 
 /* Pipeline depths the kernel that runs `desc` (with 256-byte aligned
  * operands) is compiled for: the LDS stages of the LDS-DMA kernels, 2 for
- * the register-staged generic template, 1 for the scalar kernel.  Writes up
+ * the register-staged generic template (and 4 for its 64x64 tiles, with
+ * three register sets of loads in flight: the default when K is split), 1
+ * for the scalar kernel.  Writes up
  * to max_depths of them, the default first, and returns their count (-1 on
  * error).  A schedule's unroll of the K-slab loop selects one
  * (MlirCompilerPasses.py:579-596 unrolls loops by the scheduled factor; here

@@ -896,6 +896,44 @@ def test_every_pipeline_depth(case):
         np.testing.assert_array_equal(_run_depth(ar, br, dtype, tile, split_k, depth, trans_b), default)
 
 
+# the generic template's ring instances (64x64 tiles): three register sets
+# of loads in flight; one and two slabs, slab counts that are not multiples
+# of 3, ragged M, N, K, one split and several
+RING_CASES = [
+    ("float32", (64, 64, 32, 2, 2), 4, (512, 512, 512)),
+    ("float32", (64, 64, 32, 2, 2), 1, (200, 224, 240)),
+    ("float32", (64, 64, 16, 2, 2), 2, (130, 72, 80)),
+    ("float32", (64, 64, 16, 2, 2), 1, (64, 64, 16)),
+    ("float32", (64, 64, 16, 2, 2), 1, (64, 64, 32)),
+    ("bfloat16", (64, 64, 64, 2, 2), 4, (256, 256, 2048)),
+    ("bfloat16", (64, 64, 32, 2, 2), 1, (96, 160, 224)),
+]
+
+
+@pytest.mark.parametrize("case", RING_CASES, ids=[f"{c[0]}-{c[1]}-sk{c[2]}-{c[3]}" for c in RING_CASES])
+def test_generic_ring_depth(case):
+    dtype, tile, split_k, (M, N, K) = case
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, M=M, N=N, K=K,
+                        tile=capi.Tile(*tile), split_k=split_k)
+    depths = capi.matmul_pipeline_depths(d)
+    kps = -(-(-(-K // split_k)) // tile[2]) * tile[2]
+    assert depths == ([4, 2] if -(-K // kps) > 1 else [2, 4]), depths
+    ai, bi = ref.np_init((M, K), "float32"), ref.np_init((K, N), "float32")
+    want_int = ref.matmul(ai, bi).astype(np.float32)
+    ar, br = rng_uniform(13, (M, K)), rng_uniform(14, (K, N))
+    if dtype == "bfloat16":
+        ar, br = ref.round_bf16(ar), ref.round_bf16(br)
+    base = _run_depth(ar, br, dtype, tile, split_k, 2, False)
+    err = ref.scaled_error(base, ref.matmul(ar, br), K, np.abs(ar).max(), np.abs(br).max())
+    assert err <= (TOL_F32 if dtype == "float32" else TOL_BF16), err
+    for depth in (2, 4):
+        print(f"[ring] depth {depth}", flush=True)
+        np.testing.assert_array_equal(_run_depth(ai, bi, dtype, tile, split_k, depth, False), want_int)
+        # the same slabs in the same order: bit-identical
+        np.testing.assert_array_equal(_run_depth(ar, br, dtype, tile, split_k, depth, False), base)
+    np.testing.assert_array_equal(_run_depth(ar, br, dtype, tile, split_k, 0, False), base)
+
+
 @needs_specialised
 def test_unsupported_pipeline_depth_is_an_error():
     a, b = rng_uniform(1, (512, 64)), rng_uniform(2, (64, 256))

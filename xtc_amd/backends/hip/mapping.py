@@ -12,8 +12,8 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
   * second tile level of M / N       -> wave tile WM / WN, so WGM = BM/WM,
                                         WGN = BN/WN (absent: library choice)
   * first tile level of the K dims   -> BK (LDS slab depth)
-  * parallelize(k)                   -> split-K: K / (first k level) slices
-                                        reduced by a second kernel; BK is then
+  * parallelize(k)                   -> split-K: K / (first k level) slices,
+                                        summed inside the launch; BK is then
                                         the second k level
   * interchange with N's base loop outside M's -> column-major tile raster;
     otherwise tiles are rastered in groups of 8 tile-rows (L2 reuse)
@@ -23,10 +23,11 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
     (xtc_hip_matmul_pipeline_depths: 3-6 for the fp32 LDS-DMA BK-16 tiles,
     2-3 for its BK-32 256-wide tiles, 2-4 for 128x128, 3-5 for the bf16
     ping-pong kernel, 2-4 for the skinny bf16 kernel, 2 for the generic
-    template); absent, the kernel's default.  Unroll factors of the other
-    loops are recorded: the MFMA loop over a slab and the wave's sub-tiles
-    are always fully unrolled, and the block and wave tiles are spread over
-    waves and lanes
+    template and 4 on its 64x64 tiles, which keep three slabs of loads in
+    flight in registers); absent, the kernel's default.  Unroll factors of
+    the other loops are recorded: the MFMA loop over a slab and the wave's
+    sub-tiles are always fully unrolled, and the block and wave tiles are
+    spread over waves and lanes
   * vectorize(loop) -> the 16-byte loads and stores of every kernel (4 fp32
     or 8 bf16 elements): the vectorized loop's extent must be a multiple of
     that width, or the schedule is rejected

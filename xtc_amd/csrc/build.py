@@ -141,6 +141,13 @@ def instances() -> list[tuple[int, int, int, int, int, int, int]]:
     return sorted(set(out))
 
 
+def ring_tile(dtype: int, conv: int, bm: int, bn: int, bk: int, wgm: int, wgn: int) -> bool:
+    """Tiles that also get a ring-3 instance (three register sets of global
+    loads in flight, pipeline depth 4): the 64x64 tiles that default_tile
+    picks, with split-K, for few tiles over a deep K."""
+    return (bm, bn, wgm, wgn) == (64, 64, 2, 2) and bk in ((16, 32) if dtype == F32 else (32, 64))
+
+
 def _ctype(dtype: int) -> str:
     return "float" if dtype == F32 else "__bf16"
 
@@ -160,18 +167,20 @@ def generate(parts: int = 16) -> list[Path]:
         ]
         for dtype, conv, bm, bn, bk, wgm, wgn in chunk:
             c = "true" if conv else "false"
-            lines.append(
-                f"template __global__ void gemm_kernel<{_ctype(dtype)}, {bm}, {bn}, {bk}, "
-                f"{wgm}, {wgn}, {c}>(GemmArgs);"
-            )
+            for ring in (1, 3) if ring_tile(dtype, conv, bm, bn, bk, wgm, wgn) else (1,):
+                lines.append(
+                    f"template __global__ void gemm_kernel<{_ctype(dtype)}, {bm}, {bn}, {bk}, "
+                    f"{wgm}, {wgn}, {c}, {ring}>(GemmArgs);"
+                )
         lines += ["#if !defined(__HIP_DEVICE_COMPILE__)", f"extern const GemmEntry g_gemm_part{p}[] = {{"]
         for dtype, conv, bm, bn, bk, wgm, wgn in chunk:
             c = "true" if conv else "false"
+            r = "true" if ring_tile(dtype, conv, bm, bn, bk, wgm, wgn) else "false"
             lines.append(
-                f"  make_entry<{_ctype(dtype)}, {bm}, {bn}, {bk}, {wgm}, {wgn}, {c}>(),"
+                f"  make_entry<{_ctype(dtype)}, {bm}, {bn}, {bk}, {wgm}, {wgn}, {c}, {r}>(),"
             )
         if not chunk:
-            lines.append("  GemmEntry{-1, -1, 0, 0, 0, 0, 0, 0, 0, nullptr},")
+            lines.append("  GemmEntry{-1, -1, 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr},")
         lines += [
             "};",
             f"extern const int g_gemm_part{p}_n = {len(chunk)};",

@@ -40,6 +40,10 @@
 
 namespace xtc_hip {
 
+// register sets of global loads in flight in gemm_kernel (see its K loop):
+// one by default; the registry adds ring-3 instances of a few small tiles
+constexpr int kGemmRing = 1;
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -141,10 +145,11 @@ struct GemmTile {
   static_assert(B_UNITS % NT == 0 || B_UNITS < NT, "B tile must split evenly over threads");
 };
 
-template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool CONV>
+template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool CONV, int RING = kGemmRing>
 __global__ void __attribute__((amdgpu_flat_work_group_size(WGM * WGN * 64, WGM * WGN * 64)))
 __attribute__((amdgpu_waves_per_eu(1, 4)))
 gemm_kernel(GemmArgs args) {
+  static_assert(RING >= 1 && RING <= 4, "register ring depth");
   using P = GemmTile<T, BM, BN, BK, WGM, WGN, CONV>;
   constexpr int NT = P::NT;
   constexpr int VEC = P::VEC;
@@ -206,14 +211,16 @@ gemm_kernel(GemmArgs args) {
     }
   }
 
-  u32x4 areg[P::A_PER_T];
-  u32x4 breg[P::B_REGS];
+  // RING register sets of global loads: slab t lives in set t % RING, and
+  // RING slabs are in flight while one is computed from LDS
+  u32x4 areg[RING][P::A_PER_T];
+  u32x4 breg[RING][P::B_REGS];
 
   // conv: when the channel count is a multiple of BK, a slab [kt, kt+BK)
   // lies in one filter tap (r, s); its coordinates are computed once per
   // slab from the uniform kt instead of per 16-byte chunk.
   const bool tap_slabs = CONV && args.cC % BK == 0;
-  auto load_a = [&](int kt) {
+  auto load_a = [&](int kt, int slot) {
     int slab_r = 0, slab_s = 0, slab_c = 0;
     if constexpr (CONV) {
       if (tap_slabs) {
@@ -244,17 +251,17 @@ gemm_kernel(GemmArgs args) {
         int iw = a_iw0[i] + s;
         bool inb = ok && ih >= 0 && ih < args.cH && iw >= 0 && iw < args.cW;
         if (inb) {
-          areg[i] = ldg16(Ag + ((size_t)((a_base[i] + ih) * args.cW + iw) * args.cC + c));
+          areg[slot][i] = ldg16(Ag + ((size_t)((a_base[i] + ih) * args.cW + iw) * args.cC + c));
         } else {
-          areg[i] = ok ? padv : u32x4{0, 0, 0, 0};
+          areg[slot][i] = ok ? padv : u32x4{0, 0, 0, 0};
         }
       } else {
-        areg[i] = ok ? ldg16(Ag + (size_t)a_base[i] + k) : u32x4{0, 0, 0, 0};
+        areg[slot][i] = ok ? ldg16(Ag + (size_t)a_base[i] + k) : u32x4{0, 0, 0, 0};
       }
     }
   };
 
-  auto load_b = [&](int kt) {
+  auto load_b = [&](int kt, int slot) {
     if constexpr (F32) {
 #pragma unroll
       for (int i = 0; i < P::B_PER_T; ++i) {
@@ -265,7 +272,7 @@ gemm_kernel(GemmArgs args) {
         int k = kt + kr;
         int n = n0 + nc;
         bool ok = mine && k < k_end && n < args.N;
-        breg[i] = ok ? ldg16(Bg + (size_t)k * args.ldb + n) : u32x4{0, 0, 0, 0};
+        breg[slot][i] = ok ? ldg16(Bg + (size_t)k * args.ldb + n) : u32x4{0, 0, 0, 0};
       }
     } else {
       // 8x8 blocks: thread -> (k block kc, n block nb), kc fastest
@@ -280,19 +287,19 @@ gemm_kernel(GemmArgs args) {
         for (int e = 0; e < 8; ++e) {
           int k = kt + kc * 8 + e;
           bool ok = mine && k < k_end && n < args.N;
-          breg[i * 8 + e] = ok ? ldg16(Bg + (size_t)k * args.ldb + n) : u32x4{0, 0, 0, 0};
+          breg[slot][i * 8 + e] = ok ? ldg16(Bg + (size_t)k * args.ldb + n) : u32x4{0, 0, 0, 0};
         }
       }
     }
   };
 
-  auto store_tiles = [&](T* st) {
+  auto store_tiles = [&](T* st, int slot) {
     T* As = st;
     T* Bs = st + P::A_ELEMS;
 #pragma unroll
     for (int i = 0; i < P::A_PER_T; ++i) {
       if (P::A_EVEN || tid + i * NT < P::A_CHUNKS)
-        *reinterpret_cast<u32x4*>(As + a_row[i] * P::AST + a_col[i]) = areg[i];
+        *reinterpret_cast<u32x4*>(As + a_row[i] * P::AST + a_col[i]) = areg[slot][i];
     }
     if constexpr (F32) {
 #pragma unroll
@@ -301,7 +308,7 @@ gemm_kernel(GemmArgs args) {
         if (!(P::B_EVEN || c < P::B_UNITS)) continue;
         int kr = c / P::B_CHUNKS_ROW;
         int nc = (c % P::B_CHUNKS_ROW) * VEC;
-        *reinterpret_cast<u32x4*>(Bs + kr * P::BST + nc) = breg[i];
+        *reinterpret_cast<u32x4*>(Bs + kr * P::BST + nc) = breg[slot][i];
       }
     } else {
 #pragma unroll
@@ -310,7 +317,7 @@ gemm_kernel(GemmArgs args) {
         if (!(P::B_EVEN || u < P::B_UNITS)) continue;
         int kc = u % (BK / 8);
         int nb = u / (BK / 8);
-        const u32x4* r = &breg[i * 8];
+        const u32x4* r = &breg[slot][i * 8];
         // transpose: column n of the 8x8 block becomes 8 consecutive k values
 #pragma unroll
         for (int n = 0; n < 8; ++n) {
@@ -381,22 +388,41 @@ gemm_kernel(GemmArgs args) {
     }
   };
 
+  // Slabs go global -> registers (set t % RING) -> LDS (buffer t & 1) ->
+  // MFMA.  Step t issues the loads of slab t + RING into the set slab t
+  // left (stored to LDS in step t - 1), computes slab t, then stores slab
+  // t + 1, whose loads were issued RING - 1 steps earlier: the in-order
+  // vmcnt wait before that store leaves the younger sets in flight.  One
+  // barrier per step.  The steps are unrolled by RING so every set index is
+  // a constant.
   if (nk > 0) {
-    load_a(k_begin);
-    load_b(k_begin);
-    store_tiles(smem);
-    __syncthreads();
-    for (int it = 0; it < nk; ++it) {
-      T* cur = smem + (it & 1) * P::STAGE_ELEMS;
-      T* nxt = smem + ((it & 1) ^ 1) * P::STAGE_ELEMS;
-      const bool more = it + 1 < nk;
-      if (more) {
-        load_a(k_begin + (it + 1) * BK);
-        load_b(k_begin + (it + 1) * BK);
+    load_a(k_begin, 0);
+    load_b(k_begin, 0);
+    store_tiles(smem, 0);
+#pragma unroll
+    for (int r = 1; r < RING; ++r) {
+      if (r < nk) {
+        load_a(k_begin + r * BK, r);
+        load_b(k_begin + r * BK, r);
       }
-      compute(cur);
-      if (more) store_tiles(nxt);
-      __syncthreads();
+    }
+    __syncthreads();
+    for (int it0 = 0; it0 < nk; it0 += RING) {
+#pragma unroll
+      for (int u = 0; u < RING; ++u) {
+        const int it = it0 + u;
+        if (it < nk) {
+          T* cur = smem + (it & 1) * P::STAGE_ELEMS;
+          T* nxt = smem + ((it & 1) ^ 1) * P::STAGE_ELEMS;
+          if (it + RING < nk) {
+            load_a(k_begin + (it + RING) * BK, u);
+            load_b(k_begin + (it + RING) * BK, u);
+          }
+          compute(cur);
+          if (it + 1 < nk) store_tiles(nxt, (u + 1) % RING);
+          __syncthreads();
+        }
+      }
     }
   }
 

@@ -641,17 +641,42 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   *t = xtc_hip_tile{0, 0, 0, 0, 0};
 }
 
-int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m, int xcd_remap,
+// K per split (a multiple of the slab depth bk) for `split_k` requested
+// splits of K.
+int split_depth(int K, int split_k, int bk) {
+  if (split_k < 1) split_k = 1;
+  const int kps = (K + split_k - 1) / split_k;
+  return (kps + bk - 1) / bk * bk;
+}
+
+// Splits a launch runs for K, split_k and slab depth bk.
+int effective_splits(int K, int split_k, int bk) {
+  const int kps = split_depth(K, split_k, bk);
+  return (K + kps - 1) / kps;
+}
+
+// Ring instances of the generic template (three register sets of loads in
+// flight, pipeline depth 4) for entry e at `splits` splits: 0 none, 1 one
+// exists and depth 2 is the default, 2 one exists and is the default.  Split
+// K makes each workgroup's K walk short and its load latency exposed: the
+// ring is then 10-20 % faster (ResNet18_09 conv at split 16: 20.1 -> 17.6
+// us, 512^3 fp32 at split 4: 12.8 -> 11.0 us); with one split it gains
+// nothing or loses up to 6 %.
+int generic_ring(const GemmEntry* e, int splits) {
+  if (!e || !e->launch_ring) return 0;
+  return splits > 1 ? 2 : 1;
+}
+
+// `stages` 0 (default), 2 or 4 (the ring instance, when e has one).
+int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int stages, int group_m, int xcd_remap,
                        Scratch& x) {
   const hipStream_t s = x.s;
   a.tiles_m = (a.M + e->bm - 1) / e->bm;
   a.tiles_n = (a.N + e->bn - 1) / e->bn;
   a.group_m = group_m > 0 ? group_m : 8;
   a.xcd_remap = xcd_remap;
-  if (split_k < 1) split_k = 1;
-  int kps = (a.K + split_k - 1) / split_k;
-  kps = (kps + e->bk - 1) / e->bk * e->bk;
-  int splits = (a.K + kps - 1) / kps;
+  const int kps = split_depth(a.K, split_k, e->bk);
+  const int splits = (a.K + kps - 1) / kps;
   a.k_per_split = kps;
   a.partial = nullptr;
   a.counters = nullptr;
@@ -663,7 +688,8 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int group_m
     if (!a.counters) return 1;
   }
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
-  e->launch(a, grid, s);
+  const bool ring = e->launch_ring && (stages == 4 || (stages == 0 && splits > 1));
+  (ring ? e->launch_ring : e->launch)(a, grid, s);
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -1169,10 +1195,11 @@ const char* path_name(MatmulPath p) {
 }
 
 // Pipeline depths the kernel of path p compiles for tile t: LDS stages of
-// the LDS-DMA kernels, the register-staged double buffer (2) of the generic
-// template, the split-wave kernel's ring of 4 register chunks, 1 for the
-// scalar kernel.  out[0] is the default.  Returns the count.
-int path_depths(MatmulPath p, const xtc_hip_tile& t, int* out, int max) {
+// the LDS-DMA kernels, the generic template's register-staged double buffer
+// (2) and, for the tiles with a ring instance (`ring`, generic_ring), its
+// three register sets (4), the split-wave kernel's ring of register chunks,
+// 1 for the scalar kernel.  out[0] is the default.  Returns the count.
+int path_depths(MatmulPath p, const xtc_hip_tile& t, int ring, int* out, int max) {
   int tmp[16];
   int n = 0;
   switch (p) {
@@ -1203,7 +1230,9 @@ int path_depths(MatmulPath p, const xtc_hip_tile& t, int* out, int max) {
       tmp[n++] = 1;
       break;
     default:
+      if (ring == 2) tmp[n++] = 4;
       tmp[n++] = 2;
+      if (ring == 1) tmp[n++] = 4;
       break;
   }
   for (int i = 0; i < n && i < max; ++i) out[i] = tmp[i];
@@ -1211,10 +1240,10 @@ int path_depths(MatmulPath p, const xtc_hip_tile& t, int* out, int max) {
 }
 
 // 0 if `stages` (0 = default) is a depth of path p for tile t, else fails.
-int check_depth(MatmulPath p, const xtc_hip_tile& t, int stages) {
+int check_depth(MatmulPath p, const xtc_hip_tile& t, int ring, int stages) {
   if (stages == 0) return 0;
   int depths[16];
-  const int n = path_depths(p, t, depths, 16);
+  const int n = path_depths(p, t, ring, depths, 16);
   char list[96] = "";
   for (int i = 0; i < n; ++i) {
     if (depths[i] == stages) return 0;
@@ -1288,7 +1317,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   // read like A tiles); every other transposed operand gets a natural copy
   // in a staging buffer first (one HBM-bound transpose).
   if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true)) {
-    if (check_depth(MatmulPath::LdsDmaBt, t, d.stages)) return 1;
+    if (check_depth(MatmulPath::LdsDmaBt, t, 0, d.stages)) return 1;
     return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, true);
   }
   const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
@@ -1304,7 +1333,9 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   }
   MatmulPath path;
   if (natural_path(d, t, split_k, lda, ldb, ldc, A, B, C, bias, &path)) return 1;
-  if (check_depth(path, t, d.stages)) return 1;
+  const int ring =
+      path == MatmulPath::Generic ? generic_ring(find_entry(d.dtype, 0, t), effective_splits(d.K, split_k, t.bk)) : 0;
+  if (check_depth(path, t, ring, d.stages)) return 1;
   if (path == MatmulPath::Naive) {
     dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
     if (d.dtype == XTC_HIP_F32)
@@ -1329,6 +1360,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     // kernel differs
     lds_entry = *e;
     lds_entry.launch = f32_lds_variant(t, d.stages)->launch;
+    lds_entry.launch_ring = nullptr;
     e = &lds_entry;
   }
   GemmArgs a;
@@ -1345,7 +1377,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   a.ldc = ldc;
   a.relu = d.relu;
   a.relu_threshold = d.relu_threshold;
-  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, x);
+  return launch_gemm_common(a, e, split_k, path == MatmulPath::Generic ? d.stages : 0, d.group_m, d.xcd_remap, x);
 }
 
 }  // namespace
@@ -1620,7 +1652,9 @@ int xtc_hip_matmul_pipeline_depths(const xtc_hip_matmul_desc* desc, int* depths,
     if (d.trans_b) ldb = d.N;
     if (natural_path(d, t, split_k, lda, ldb, ldc, p, p, p, nullptr, &path)) return -1;
   }
-  return path_depths(path, t, depths, max_depths);
+  const int ring =
+      path == MatmulPath::Generic ? generic_ring(find_entry(d.dtype, 0, t), effective_splits(d.K, split_k, t.bk)) : 0;
+  return path_depths(path, t, ring, depths, max_depths);
 }
 
 int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths, int max_depths) {
@@ -1645,11 +1679,13 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
                  t.wgm, t.wgn);
   const void* p = (const void*)(uintptr_t)256;
   // the direct kernel keeps its weight taps in LDS stages or a register
-  // ring; the implicit-GEMM loader double-buffers through registers
+  // ring; the implicit-GEMM loader double-buffers through registers, with
+  // three register sets in flight on the tiles that have a ring instance
+  // when K is split
   if (direct_conv_applies(d, t, split_k, OH, OW, p, p, p, nullptr))
     depths[0] = direct_conv_tile(t)->depth();
   else if (e->launch)
-    depths[0] = 2;
+    depths[0] = generic_ring(e, effective_splits(d.R * d.S * d.C, split_k > 0 ? split_k : 1, t.bk)) == 2 ? 4 : 2;
   else
     return -fail("conv2d tile %dx%dx%d waves %dx%d exists only in the direct conv kernel, which does not take "
                  "this shape",
@@ -1789,7 +1825,7 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   a.cPW = d.pad_left;
   a.pad_value = d.pad_value;
   Scratch x{s};
-  return launch_gemm_common(a, e, split_k, d.group_m, d.xcd_remap, x);
+  return launch_gemm_common(a, e, split_k, 0, d.group_m, d.xcd_remap, x);
 }
 
 int xtc_hip_relu(const float* x, float* y, uint64_t n, float threshold, void* stream) {
