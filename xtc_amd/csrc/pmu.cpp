@@ -82,8 +82,13 @@ rocprofiler_status_t collect_agents(rocprofiler_agent_version_t, const void** ag
   return ROCPROFILER_STATUS_SUCCESS;
 }
 
+// rocprofiler calls the two callbacks below from its own code paths; they
+// take g_mu, so this file never calls into rocprofiler while holding g_mu
+// (a rocprofiler lock held around a callback would otherwise order against
+// g_mu both ways).
 void dispatch_cb(rocprofiler_dispatch_counting_service_data_t data, rocprofiler_counter_config_id_t* config,
                  rocprofiler_user_data_t*, void*) {
+  std::lock_guard<std::mutex> lk(g_mu);
   if (!g_have_config || data.dispatch_info.agent_id.handle != g_config_agent.handle) return;
   *config = g_config;
   g_issued.fetch_add(1);
@@ -91,12 +96,20 @@ void dispatch_cb(rocprofiler_dispatch_counting_service_data_t data, rocprofiler_
 
 void record_cb(rocprofiler_dispatch_counting_service_data_t, rocprofiler_counter_record_t* records, size_t n,
                rocprofiler_user_data_t, void*) {
-  std::lock_guard<std::mutex> lk(g_mu);
+  // decode the records first, then add them up under g_mu
+  std::vector<std::pair<uint64_t, double>> vals;
+  vals.reserve(n);
   for (size_t i = 0; i < n; ++i) {
     rocprofiler_counter_id_t cid{0};
-    if (rocprofiler_query_record_counter_id(records[i].id, &cid) != ROCPROFILER_STATUS_SUCCESS) continue;
-    auto it = g_slot_of_counter.find(cid.handle);
-    if (it != g_slot_of_counter.end()) g_sums[it->second] += records[i].counter_value;
+    if (rocprofiler_query_record_counter_id(records[i].id, &cid) == ROCPROFILER_STATUS_SUCCESS)
+      vals.emplace_back(cid.handle, records[i].counter_value);
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const auto& v : vals) {
+      auto it = g_slot_of_counter.find(v.first);
+      if (it != g_slot_of_counter.end()) g_sums[it->second] += v.second;
+    }
   }
   g_completed.fetch_add(1);
 }
@@ -267,19 +280,24 @@ int xtc_hip_pmu_open(int device, int n, const char** names, int* slots) {
     slot_of[it->second.handle] = (int)chosen.size();
     chosen.push_back(it->second);
   }
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (g_have_config) {
-    rocprofiler_destroy_counter_config(g_config);
+  // take the open configuration out under g_mu, destroy it and create the
+  // new one without it, then publish the new one under g_mu
+  rocprofiler_counter_config_id_t old{0};
+  bool had = false;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    had = g_have_config;
+    old = g_config;
     g_have_config = false;
+    g_slot_of_counter = slot_of;
+    g_sums.assign(chosen.size(), 0.0);
   }
-  g_slot_of_counter = slot_of;
-  g_sums.assign(chosen.size(), 0.0);
+  if (had) rocprofiler_destroy_counter_config(old);
   if (chosen.empty()) return 0;
   rocprofiler_counter_config_id_t cfg{0};
-  if (rocprofiler_create_counter_config(a->id, chosen.data(), chosen.size(), &cfg) != ROCPROFILER_STATUS_SUCCESS) {
-    g_error = "rocprofiler_create_counter_config failed (unsupported set, or more counters than one pass holds)";
-    return 1;
-  }
+  if (rocprofiler_create_counter_config(a->id, chosen.data(), chosen.size(), &cfg) != ROCPROFILER_STATUS_SUCCESS)
+    return fail("rocprofiler_create_counter_config failed (unsupported set, or more counters than one pass holds)");
+  std::lock_guard<std::mutex> lk(g_mu);
   g_config = cfg;
   g_config_agent = a->id;
   g_have_config = true;
@@ -319,11 +337,17 @@ int xtc_hip_pmu_stop(double* sums, int n) {
 
 // Drops the open configuration.
 void xtc_hip_pmu_close(void) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (g_have_config) rocprofiler_destroy_counter_config(g_config);
-  g_have_config = false;
-  g_slot_of_counter.clear();
-  g_sums.clear();
+  rocprofiler_counter_config_id_t old{0};
+  bool had = false;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    had = g_have_config;
+    old = g_config;
+    g_have_config = false;
+    g_slot_of_counter.clear();
+    g_sums.clear();
+  }
+  if (had) rocprofiler_destroy_counter_config(old);
 }
 
 }  // extern "C"
