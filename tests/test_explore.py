@@ -408,3 +408,43 @@ def test_cli_descript_spec_replaces_the_strategy(tmp_path, monkeypatch):
     assert list(rows[0])[:5] == ["bm", "bn", "bk", "wm", "wn"] and len(rows) == 4
     db = [json.loads(l) for l in open(tmp_path / "d.jsonl")]
     assert all(d["strategy"][2] == "descript" and d["kernels"]["C"].startswith("gemm<float32>") for d in db)
+
+
+# ---------------------------------------------------------------- the reference's Python form
+
+def test_exploration_from_a_configuration(tmp_path, monkeypatch, capsys):
+    """Exploration(config): the graph from the configuration's operator and
+    dims, every backend of `backends`, results as (sample, code, time,
+    backend) in the return value, `results` and `config.results`, and the
+    reference's closing line (src/xtc/search/explore.py:200-210, 764-873;
+    docs/tutorials/explore_optimizers.py:199-227)."""
+    monkeypatch.setattr(Exploration, "evaluate_one", lambda self, module: ([2e-4, 1e-4], 0, ""))
+    config = ExplorationConfig(operator="matmul", dims=[256, 256, 256], backends=["hip"], strategy="tile_hip",
+                               search="random", trials=3, seed=0, output=str(tmp_path / "r.csv"), peak_flops=1e12,
+                               func_name="mm")
+    exploration = Exploration(config)
+    res = exploration()
+    assert res is exploration.results and config.results == res and len(res) == 3
+    assert all(code == 0 and t == 1e-4 and backend == "hip" and len(x) == 7 for x, code, t, backend in res)
+    assert capsys.readouterr().out.startswith("Schedule: hip: [")
+    rows = list(csv.DictReader(open(tmp_path / "r.csv")))
+    assert len(rows) == 3 and float(rows[0]["peak"]) == pytest.approx(256**3 / 1e12 / 1e-4)
+    # a named operation's dims, opt-level 0-3: one default schedule
+    config = ExplorationConfig(operator="conv2d", op_name="ResNet18_12", opt_level=2, quiet=True,
+                               output=str(tmp_path / "n.csv"), peak_flops=1e12)
+    (res,) = Exploration(config).run()
+    assert res[1] == 0 and capsys.readouterr().out == ""
+    # a reference strategy with its scheme argument (prt:<scheme>), filtered to compiled kernels
+    config = ExplorationConfig(operator="matmul", dims=[512, 512, 512], strategy="prt:PPRPRP", trials=2, quiet=True,
+                               output=str(tmp_path / "p.csv"), peak_flops=1e12)
+    assert [code for _, code, _, _ in Exploration(config).run()] == [0, 0]
+
+
+def test_exploration_config_from_args():
+    import argparse
+
+    ns = argparse.Namespace(operator="conv2d", trials=7, search="exhaustive", not_a_field=1)
+    c = ExplorationConfig.from_args(ns, seed=3)
+    assert (c.operator, c.trials, c.search, c.seed) == ("conv2d", 7, "exhaustive", 3)
+    with pytest.raises(TypeError, match="unknown exploration configuration option"):
+        ExplorationConfig.from_args(None, trialz=1)

@@ -28,55 +28,16 @@ import os
 import sys
 from typing import Any
 
-from ..search.explore import Exploration, ExplorationConfig
+from ..search.explore import OPERATORS, Exploration, ExplorationConfig, build_graph, operation_dims
 from ..search.strategies import Strategies
 
-# default dims of the reference's OPERATORS table (src/xtc/search/explore.py:150-198)
-DEFAULT_DIMS = {"matmul": [512, 1024, 128], "conv2d": [1, 112, 112, 64, 7, 7, 3, 2, 2], "relu": [512 * 1024]}
+# default dims of the reference's OPERATORS table (src/xtc/search/explore.py:151-198)
+DEFAULT_DIMS = {name: list(op["default_dims"]) for name, op in OPERATORS.items()}
+
+__all__ = ["main", "build_graph", "DEFAULT_DIMS"]
 
 
-def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0, name: str | None = None) -> Any:
-    """Graphs of the reference's `--operator` choices, with the same tensor
-    and node names and shapes (explore.py:218-256).  bfloat16 matmul/conv
-    accumulate and store fp32 (out_dtype extension).  `pad` > 0 puts a
-    pad2d producer on H and W in front of the conv (the C4 pattern); the
-    padded input then has the reference's conv input shape.  `name` is the
-    graph's (function's) name, default to the operator."""
-    import xtc_amd.graphs.xtc.op as O
-
-    extra = {"out_dtype": "float32"} if dtype == "bfloat16" else {}
-    if operator == "matmul":
-        i, j, k = dims
-        a = O.tensor((i, k), dtype, name="A")
-        b = O.tensor((k, j), dtype, name="B")
-        with O.graph(name=name or "matmul") as gb:
-            O.matmul(a, b, name="C", **extra)
-        return gb.graph
-    if operator == "conv2d":
-        n, h, w, f, r, s, c, sh, sw = dims if len(dims) == 9 else (dims + [1, 1])[:9]
-        ih, iw = h * sh + r - 1 - 2 * pad, w * sw + s - 1 - 2 * pad
-        x = O.tensor((n, ih, iw, c), dtype, name="A")
-        wt = O.tensor((r, s, c, f), dtype, name="B")
-        with O.graph(name=name or "conv2d") as gb:
-            src = O.pad2d(x, padding=pad, axes=(1, 2), name="pad") if pad else x
-            O.conv2d(src, wt, stride=(sh, sw), name="O", **extra)
-        return gb.graph
-    if operator == "relu":
-        (i,) = dims
-        x = O.tensor((i,), dtype, name="I")
-        with O.graph(name=name or "relu") as gb:
-            O.relu(x, threshold=0, name="O")
-        return gb.graph
-    raise SystemExit(f"unknown operator {operator}")
-
-
-def _operation_dims(operator: str, name: str) -> list[int]:
-    """Dims of a named operation: its loop sizes, then its params
-    (src/xtc/search/explore.py:837-841)."""
-    from ..artifacts import get_operation
-
-    op = get_operation(operator, name)
-    return [*op["dims"].values(), *op["params"].values()]
+_operation_dims = operation_dims
 
 
 def _bool(p: argparse.ArgumentParser, name: str, default: bool, help: str) -> None:
@@ -183,85 +144,26 @@ def main(argv: list[str] | None = None) -> int:
         except ValueError as err:
             print(err, file=sys.stderr)
             return 2
+    if args.op_name:
+        try:
+            _operation_dims(args.operator, args.op_name)
+        except ValueError as err:
+            p.error(str(err))
     if "hip" in args.backends:
         from ..backends.hip.compiler import CompileService
 
         # the payload compiler's fork server starts before anything loads the
         # GPU libraries (XTC_HIP_PMU=1 registers the counter tool on load)
         CompileService.start_server()
-
+    config = ExplorationConfig.from_args(args)
     if args.graph_file:
-        import xtc_amd.graphs.xtc.op as O
-
-        with O.graph() as gb:
-            gb.load(args.graph_file)
-        graph = gb.graph
-    else:
-        if args.op_name:
-            try:
-                dims = _operation_dims(args.operator, args.op_name)
-            except ValueError as err:
-                p.error(str(err))
-        else:
-            dims = args.dims or DEFAULT_DIMS[args.operator]
-        graph = build_graph(args.operator, dims, args.dtype, args.pad, name=args.func_name or args.operator)
-    max_unroll = args.max_unroll if args.max_unroll is not None else 1 << 22
-    strat_kwargs = {"threads": args.threads, "max_unroll": max_unroll, "vec_size": args.vec_size}
-    if args.descript or Strategies.resolve_name(args.strategy) == "tile_hip":
-        strat_kwargs = {}
-    # the reference evaluates one schedule at opt-level 0-3 or with --test
-    # (src/xtc/search/explore.py:784-800)
-    search = "default" if args.opt_level in (0, 1, 2, 3) else args.search
-    for backend in args.backends:
-        cfg = ExplorationConfig(
-            backend=backend,
-            strategy=args.strategy,
-            strategy_kwargs=strat_kwargs,
-            search=search,
-            trials=args.trials,
-            seed=args.seed,
-            optimizer=args.optimizer,
-            optimizer_config=args.optimizer_config,
-            batch=args.batch,
-            opt_level=min(args.opt_level, 3),
-            data=args.data,
-            repeat=args.repeat,
-            number=args.number,
-            min_repeat_ms=args.min_repeat_ms,
-            validate=args.validate,
-            pmu_counters=args.pmu_counters,
-            jobs=args.jobs,
-            output=args.output,
-            db_file=args.db_file,
-            resume=args.resume,
-            append=args.append,
-            peak_flops=args.peak_flops,
-            compile_kwargs={"debug": True} if args.debug_compile else {},
-            test=args.test,
-            execute=args.execute,
-            quiet=args.quiet,
-            dump=args.dump,
-            save_temps=args.save_temps,
-            save_temps_dir=args.save_temps_dir,
-            explore_dir=args.explore_dir,
-            descript=args.descript,
-        )
-        exploration = Exploration(graph, cfg)
-        results = exploration.run()
-        if args.quiet:
-            continue
-        if not args.execute:
-            ok = sum(1 for _, _, code, _ in results if code == 0)
-            print(f"{backend}: compiled {ok}/{len(results)} samples", flush=True)
-            continue
-        ok = [(min(t), s) for s, t, code, _ in results if code == 0 and t]
-        if ok:
-            best_t, best_s = min(ok)
-            peak = exploration.peak_time_s / best_t if exploration.peak_time_s else 0.0
-            print(f"Schedule: {backend}: {best_s}: time: {best_t * 1000:.2f} msecs, peak perf: {peak * 100:.2f}%",
-                  flush=True)
-        else:
-            print(f"{backend}: no successful sample ({len(results)} tried)", flush=True)
+        config.operator = None
+    results = Exploration(config).run()
+    if not args.quiet and not args.execute:
+        ok = sum(1 for _, code, _, _ in results if code == 0)
+        print(f"compiled {ok}/{len(results)} samples", flush=True)
+    elif not args.quiet and not any(code == 0 and t > 0 for _, code, t, _ in results):
+        print(f"no successful sample ({len(results)} tried)", flush=True)
     return 0
 
 

@@ -38,7 +38,7 @@ import platform
 import subprocess
 import sys
 import time
-from dataclasses import asdict, dataclass, field
+from dataclasses import dataclass, field, fields
 from datetime import datetime, timezone
 from importlib import import_module
 from pathlib import Path
@@ -46,23 +46,32 @@ from typing import Any, Callable
 
 from .strategies import Strategies
 
-__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x"]
+__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x", "OPERATORS",
+           "build_graph", "operation_dims", "config_graph"]
 
 logger = logging.getLogger("xtc_amd.search")
 
 
 @dataclass
 class ExplorationConfig:
+    """Options of an exploration (src/xtc/search/explore.py:65-148).  The
+    reference's fields are all here, with its defaults except `strategy`
+    (tile_hip, the GPU-native space), `repeat` (5: the minimum of five
+    timed repeats) and `backends` (hip).  `backend` is the one backend an
+    `Exploration(graph, config)` runs; `Exploration(config)` builds the
+    graph from `operator`/`dims`/`dtype` (or `op_name`, or `graph_file`)
+    and runs every backend of `backends`."""
+
     backend: str = "hip"
     strategy: str = "tile_hip"
     strategy_kwargs: dict[str, Any] = field(default_factory=dict)
     search: str = "random"  # "random" | "exhaustive" | "data" | "default" | "iterative"
-    trials: int = 64
+    trials: int = 100
     seed: int = 0
     optimizer: str = "random-forest-default"  # search "iterative"
     optimizer_config: str = ""  # YAML overrides of the optimizer preset
     batch: int = 1  # samples per optimizer proposal
-    opt_level: int = 2
+    opt_level: int = 4  # 0-3: evaluate the strategy's default schedule at that level; 4: search
     data: str | None = None  # CSV of samples for search "data"
     repeat: int = 5
     number: int = 1
@@ -84,6 +93,122 @@ class ExplorationConfig:
     save_temps_dir: str = "./save_temps_dir"
     explore_dir: str | None = None  # where the payload libraries go (dump_file = <dir>/payload_<ident>)
     descript: str | None = None  # path to a descript YAML spec; replaces `strategy` when set
+    # the graph, for Exploration(config): an operator of OPERATORS with its
+    # dims (default: the operator's), a named operation's dims, or a file
+    operator: str | None = "matmul"
+    graph_file: str | None = None
+    op_name: str | None = None
+    func_name: str | None = None  # graph (payload) name, default to the operator
+    dims: list[int] | None = None
+    dtype: str = "float32"
+    pad: int = 0  # conv2d: a pad2d producer on H and W (an extension)
+    backends: list[str] = field(default_factory=lambda: ["hip"])
+    # options of the reference's strategies (not tile_hip, which takes none)
+    threads: int = 1
+    max_unroll: int | None = None  # default 2^22: GPU tiles unroll further than the CPU bound of 256
+    vec_size: int = 16
+    # accepted for compatibility; they change nothing on this backend
+    huge_pages: bool = True
+    eval: str = "eval"
+    bare_ptr: bool = False
+    mlir_prefix: str | None = None
+    use_tensors: bool = False
+    progress_cls: str = "tqdm"
+    debug_compile: bool = False  # log the payload compile commands
+    eval_parameters: Any = None  # (inputs, outputs) numpy arrays for every evaluation
+    # filled by Exploration(config).run(): (sample, code, time, backend) per sample
+    results: list[Any] = field(default_factory=list)
+
+    @classmethod
+    def from_args(cls, args: Any = None, **overrides: Any) -> "ExplorationConfig":
+        """A configuration from an argparse namespace (its attributes that
+        name fields) and keyword overrides (src/xtc/search/explore.py:133-148)."""
+        config = cls()
+        names = {f for f in cls.__dataclass_fields__}
+        if args is not None:
+            for key, value in vars(args).items():
+                if key in names:
+                    setattr(config, key, value)
+        for key, value in overrides.items():
+            if key not in names:
+                raise TypeError(f"unknown exploration configuration option: {key}")
+            setattr(config, key, value)
+        return config
+
+
+# configuration fields left out of the run manifest: data, not options
+_NOT_IN_MANIFEST = ("results", "eval_parameters")
+
+# Operators of `operator` (src/xtc/search/explore.py:151-198): dimension
+# names and default dims.
+OPERATORS: dict[str, dict[str, Any]] = {
+    "matmul": {"dims": ["i", "j", "k"], "default_dims": [512, 1024, 128]},
+    "conv2d": {"dims": ["n", "h", "w", "f", "r", "s", "c", "SH", "SW"], "default_dims": [1, 112, 112, 64, 7, 7, 3, 2, 2]},
+    "relu": {"dims": ["i"], "default_dims": [512 * 1024]},
+}
+
+
+def operation_dims(operator: str, name: str) -> list[int]:
+    """Dims of a named operation: its loop sizes, then its params
+    (src/xtc/search/explore.py:837-841)."""
+    from ..artifacts import get_operation
+
+    op = get_operation(operator, name)
+    return [*op["dims"].values(), *op["params"].values()]
+
+
+def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0, name: str | None = None) -> Any:
+    """Graphs of the reference's operators, with the same tensor and node
+    names and shapes (src/xtc/search/explore.py:218-256).  bfloat16
+    matmul/conv accumulate and store fp32 (out_dtype extension).  `pad` > 0
+    puts a pad2d producer on H and W in front of the conv (the C4 pattern);
+    the padded input then has the reference's conv input shape.  `name` is
+    the graph's (function's) name, default to the operator."""
+    import xtc_amd.graphs.xtc.op as O
+
+    extra = {"out_dtype": "float32"} if dtype == "bfloat16" else {}
+    if operator == "matmul":
+        i, j, k = dims
+        a = O.tensor((i, k), dtype, name="A")
+        b = O.tensor((k, j), dtype, name="B")
+        with O.graph(name=name or "matmul") as gb:
+            O.matmul(a, b, name="C", **extra)
+        return gb.graph
+    if operator == "conv2d":
+        n, h, w, f, r, s, c, sh, sw = dims if len(dims) == 9 else (list(dims) + [1, 1])[:9]
+        ih, iw = h * sh + r - 1 - 2 * pad, w * sw + s - 1 - 2 * pad
+        x = O.tensor((n, ih, iw, c), dtype, name="A")
+        wt = O.tensor((r, s, c, f), dtype, name="B")
+        with O.graph(name=name or "conv2d") as gb:
+            src = O.pad2d(x, padding=pad, axes=(1, 2), name="pad") if pad else x
+            O.conv2d(src, wt, stride=(sh, sw), name="O", **extra)
+        return gb.graph
+    if operator == "relu":
+        (i,) = dims
+        x = O.tensor((i,), dtype, name="I")
+        with O.graph(name=name or "relu") as gb:
+            O.relu(x, threshold=0, name="O")
+        return gb.graph
+    raise ValueError(f"unknown operator {operator}")
+
+
+def config_graph(config: ExplorationConfig) -> Any:
+    """The graph an Exploration(config) explores: the graph file, else the
+    operator with the named operation's dims, the given dims or its
+    default ones."""
+    if config.graph_file:
+        import xtc_amd.graphs.xtc.op as O
+
+        with O.graph() as gb:
+            gb.load(config.graph_file)
+        return gb.graph
+    if not config.operator or config.operator not in OPERATORS:
+        raise ValueError(f"unknown operator {config.operator!r}: one of {list(OPERATORS)}")
+    if config.op_name:
+        dims = operation_dims(config.operator, config.op_name)
+    else:
+        dims = list(config.dims) if config.dims else list(OPERATORS[config.operator]["default_dims"])
+    return build_graph(config.operator, dims, config.dtype, config.pad, name=config.func_name or config.operator)
 
 
 class CSVCallback:
@@ -235,34 +360,70 @@ def check_explore_counters(names: list[str]) -> None:
 
 
 class Exploration:
-    def __init__(self, graph: Any, config: ExplorationConfig) -> None:
+    """An exploration, in either of two forms:
+
+    * `Exploration(config)` (the reference's, src/xtc/search/explore.py:
+      200-210, 864-873): the graph comes from the configuration
+      (config_graph), every backend of `config.backends` is explored, and
+      `run()` (or calling the object) returns and keeps in `results` and
+      `config.results` one (sample, code, time, backend) per sample;
+    * `Exploration(graph, config)`: `config.backend` on a given graph;
+      `run()` returns (sample, times, code, message) per sample.
+    """
+
+    def __init__(self, graph: Any = None, config: ExplorationConfig | None = None) -> None:
+        self.results: list[Any] = []
+        if config is None and (graph is None or isinstance(graph, ExplorationConfig)):
+            self.config = graph if graph is not None else ExplorationConfig()
+            self.graph = None
+            self.strategy = None
+            self.peak_time_s = 0.0
+            return
+        assert config is not None, "Exploration(graph, config) needs a configuration"
         self.graph = graph
         self.config = config
         self._backend_mod = import_module(f"xtc_amd.backends.{config.backend}")
         factory = self._strategy_factory(graph, config)
-        kwargs = dict(config.strategy_kwargs)
-        if config.backend == "hip" and (config.descript or Strategies.resolve_name(config.strategy) != "tile_hip"):
+        kwargs: dict[str, Any] = {}
+        if config.backend == "hip" and (config.descript or self.strategy_name(config.strategy) != "tile_hip"):
             kwargs["sample_filter"] = hip_sample_filter(graph, factory)
         self.strategy = factory(**kwargs)
         self.peak_time_s = 0.0  # the graph's time at peak, set by run()
 
     @staticmethod
+    def strategy_name(strategy: str) -> str:
+        """The registered name of `strategy`, whose arguments follow a colon
+        (`prt:PPRPRP`; src/xtc/search/explore.py:813-834)."""
+        return Strategies.resolve_name(strategy.split(":")[0])
+
+    @staticmethod
     def _strategy_factory(graph: Any, config: ExplorationConfig) -> Callable[..., Any]:
         """Strategy constructor: a descript spec file replaces the named
-        strategy (src/xtc/search/explore.py:817-834)."""
+        strategy; the reference's strategies get `threads`, `max_unroll`
+        and `vec_size` (src/xtc/search/explore.py:817-834), tile_hip takes
+        no option; `strategy_kwargs` override them."""
         if config.descript:
             from .descript_strategy import Strategy_Descript
 
             with open(config.descript) as f:
                 spec = f.read()
             return lambda **kw: Strategy_Descript(graph, spec, **{**config.strategy_kwargs, **kw})
-        return lambda **kw: Strategies.create(config.strategy, graph, **{**config.strategy_kwargs, **kw})
+        name, *args = config.strategy.split(":")
+        options: dict[str, Any] = {}
+        if Strategies.resolve_name(name) != "tile_hip":
+            options = {"threads": config.threads, "vec_size": config.vec_size,
+                       "max_unroll": config.max_unroll if config.max_unroll is not None else 1 << 22}
+        return lambda **kw: Strategies.create(name, graph, *args, **{**options, **config.strategy_kwargs, **kw})
 
     # ---- sample sources
     def samples(self) -> list[list[int]]:
         c = self.config
         if c.test:
             return [list(c.test)]
+        # opt-level 0-3 evaluates the strategy's default schedule at that
+        # level, whatever the search (src/xtc/search/explore.py:784-800)
+        if c.opt_level in (0, 1, 2, 3):
+            return [list(self.strategy.default_schedule(c.opt_level))]
         if c.search == "exhaustive":
             from itertools import islice
 
@@ -275,7 +436,7 @@ class Exploration:
             with open(c.data, newline="") as f:
                 return [parse_x(row["X"]) for row in csv.DictReader(f)]
         if c.search == "default":
-            return [list(self.strategy.default_schedule(c.opt_level))]
+            return [list(self.strategy.default_schedule(2))]
         raise ValueError(f"unknown search {c.search!r}")
 
     # ---- one sample
@@ -289,6 +450,8 @@ class Exploration:
             kwargs.setdefault("dump_file", f"{c.explore_dir}/payload_{ident}")
         if c.dump:
             kwargs.setdefault("print_source_ir", True)
+        if c.debug_compile:
+            kwargs.setdefault("debug", True)
         if c.save_temps:
             kwargs.setdefault("save_temps", True)
             kwargs.setdefault("save_temps_dir", f"{c.save_temps_dir}/{ident}")
@@ -310,7 +473,7 @@ class Exploration:
         check_explore_counters(c.pmu_counters)
         return module.get_evaluator(
             repeat=c.repeat, number=c.number, min_repeat_ms=c.min_repeat_ms, validate=c.validate,
-            pmu_counters=self.counters(),
+            pmu_counters=self.counters(), parameters=c.eval_parameters,
         ).evaluate()
 
     def split_counters(self, values: list[float]) -> tuple[list[float], dict[str, list[float]]]:
@@ -343,8 +506,9 @@ class Exploration:
             "gitCommit": commit,
             "python": {"version": sys.version, "executable": sys.executable},
             "platform": {"platform": sys.platform, "machine": platform.machine(), "cwd": os.getcwd()},
-            "args": {k: (v if isinstance(v, (str, int, float, bool, list, dict, type(None))) else str(v))
-                     for k, v in asdict(self.config).items()},
+            "args": {f.name: (v if isinstance(v, (str, int, float, bool, list, dict, type(None))) else str(v))
+                     for f in fields(self.config) if f.name not in _NOT_IN_MANIFEST
+                     for v in [getattr(self.config, f.name)]},
         }
         Path(f"{self.config.output}.meta.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
 
@@ -391,7 +555,42 @@ class Exploration:
                 logger.info("[%d/%d] %s -> %.3g s (%s)", done + idx + 1, total, sample, best, res[3] or "ok")
         return out
 
-    def run(self) -> list[tuple[list[int], list[float], int, str]]:
+    def __call__(self) -> list[Any]:
+        return self.run()
+
+    def run(self) -> list[Any]:
+        if self.graph is None:
+            return self._run_config()
+        return self._run_graph()
+
+    def _run_config(self) -> list[tuple[list[int], int, float, str]]:
+        """Exploration(config): every backend of config.backends on the
+        configuration's graph; one (sample, code, time, backend) per sample,
+        time the minimum over repeats (0 when the sample failed), and the
+        best sample's line unless quiet (src/xtc/search/explore.py:764-811)."""
+        from dataclasses import replace
+
+        c = self.config
+        graph = config_graph(c)
+        out: list[tuple[list[int], int, float, str]] = []
+        best: tuple[float, list[int], str, float] | None = None
+        for backend in c.backends:
+            sub = Exploration(graph, replace(c, backend=backend, results=[]))
+            for sample, times, code, _ in sub.run():
+                t = min(times) if code == 0 and times else 0.0
+                out.append((list(sample), code, t, backend))
+                if t > 0 and (best is None or t < best[0]):
+                    best = (t, list(sample), backend, sub.peak_time_s / t if sub.peak_time_s else 0.0)
+        if best is not None and not c.quiet:
+            t, sample, backend, peak = best
+            print(f"Schedule: {backend}: {sample}: time: {t * 1000:.2f} msecs, peak perf: {peak * 100:.2f}%",
+                  flush=True)
+        self.results = out
+        c.results = out
+        return out
+
+    # ---- the exploration proper
+    def _run_graph(self) -> list[tuple[list[int], list[float], int, str]]:
         from contextlib import nullcontext
 
         c = self.config
@@ -404,10 +603,8 @@ class Exploration:
             self.write_manifest()  # runs git: before any GPU work
             results: list[tuple[list[int], list[float], int, str]] = []
             t0 = time.time()
-            if c.search == "iterative":
-                samples: list[list[int]] = []
-            else:
-                samples = self.samples()
+            iterative = c.search == "iterative" and not c.test and c.opt_level not in (0, 1, 2, 3)
+            samples: list[list[int]] = [] if iterative else self.samples()
             # compile-only runs never touch the GPU
             peak_time = self.peak_time() if c.execute else 0.0
             self.peak_time_s = peak_time
@@ -415,10 +612,10 @@ class Exploration:
                 Path(c.save_temps_dir).mkdir(parents=True, exist_ok=True)
                 self.graph.dump(str(Path(c.save_temps_dir) / f"{self.graph.name}.graph.yaml"))
             csv_cb = CSVCallback(c.output, peak_time, self.strategy.sample_names, resume=c.resume, append=c.append)
-            db_cb = DBCallback(c.db_file, self.graph, "descript" if c.descript else c.strategy) if c.db_file else None
+            db_cb = DBCallback(c.db_file, self.graph, "descript" if c.descript else self.strategy_name(c.strategy)) if c.db_file else None
             try:
                 with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
-                    if c.search == "iterative":
+                    if iterative:
                         results = self._run_iterative(pool, csv_cb, db_cb, peak_time)
                     else:
                         todo = [s for s in samples if (c.backend, tuple(s)) not in csv_cb.seen]
