@@ -217,3 +217,20 @@ def test_hip_filter_keeps_samples_that_map_to_compiled_kernels():
         (ln,) = [l for l in backend.plan.launches if l.kind == "matmul"]
         map_node(ln.attrs, False, sch.schedule().node("C"), "strict")
     assert s.stats["filtered"] > 0
+
+
+def test_reference_import_path_and_dict_samples():
+    """The reference imports the strategy from xtc.search.strategies and
+    applies dict samples (src/xtc/search/strategies.py:1031-1185)."""
+    from xtc_amd.search.strategies import Strategy_Descript as S, Strategy_Descript_Explore
+
+    assert S is Strategy_Descript and Strategy_Descript_Explore is Strategy_Descript
+    spec, extra, _, _ = GOLDEN["simple"]
+    g = _mm()
+    s = S(g, spec, constraints=extra, initialize=False)
+    x = s.default_schedule()
+    a, b = Backend(g).get_scheduler(), Backend(g).get_scheduler()
+    s.generate(a, x)
+    s.generate(b, s.sample_to_dict(x))
+    assert str(a.schedule()) == str(b.schedule())
+

@@ -46,7 +46,7 @@ from ..itf.search import Sample, Strategy, VecSample
 from ..schedules.descript import Descript, compile_expr
 from ..utils.algorithms import sample_uniques
 
-__all__ = ["Strategy_Descript"]
+__all__ = ["Strategy_Descript", "Strategy_Descript_Explore"]
 
 # a complete enumeration is attempted up to this many solver steps; above
 # it, samples come from randomised depth-first draws
@@ -366,8 +366,11 @@ class Strategy_Descript(Strategy):
     def stats(self) -> Mapping[str, int]:
         return self._stats
 
-    def generate(self, scheduler: Any, sample: Sample) -> None:
-        self._descript.apply_sample(self._nest, dict(zip(self._params, sample)), scheduler)
+    def generate(self, scheduler: Any, sample: Sample | Mapping[str, int]) -> None:
+        """Applies a sample: a list in `sample_names` order, or a mapping
+        from parameter to value (the reference's Strategy_Descript form)."""
+        env = dict(sample) if isinstance(sample, Mapping) else dict(zip(self._params, sample))
+        self._descript.apply_sample(self._nest, env, scheduler)
 
     def exhaustive(self) -> Iterator[VecSample]:
         sols = self._enumerate()
@@ -420,3 +423,8 @@ class Strategy_Descript(Strategy):
 
     def sample_to_dict(self, sample: Sample) -> dict[str, int]:
         return dict(zip(self._params, sample))
+
+
+# the reference's explorer-facing name (src/xtc/search/strategies.py:1156-1183):
+# samples as lists in a fixed parameter order, which Strategy_Descript does
+Strategy_Descript_Explore = Strategy_Descript

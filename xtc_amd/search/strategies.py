@@ -787,3 +787,13 @@ Strategies.register("prt", BaseStrategyPRTScheme)
 Strategies.register("tile_hip", Strategy_HIP, aliases=("tile_gpu",))
 Strategies.register_alias("tile4d", "tile_p1")
 Strategies.register_alias("tile4dv", "tile_p1_v")
+
+
+def __getattr__(name: str) -> Any:
+    # the descript strategies live in descript_strategy.py (which imports
+    # this module); they are also reachable here, as in the reference
+    if name in ("Strategy_Descript", "Strategy_Descript_Explore"):
+        from . import descript_strategy
+
+        return getattr(descript_strategy, name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
