@@ -248,14 +248,15 @@ def _elementwise(steps: int) -> int:
     return 0
 
 
-def _named_ops(steps: int, warmup_ms: float) -> int:
+def _named_ops(steps: int, warmup_ms: float, dtype: str = "float32") -> int:
     """Every named operation of `loop-explore --op-name` (the reference's
     layer registry, src/xtc/artifacts) with the backend's default schedule,
     one JSON line each: kernel time per payload call over `steps`
     back-to-back calls at steady clocks (HIP events, seeded uniform inputs),
-    TFLOP/s, and the fraction of the op's roofline max(FLOP / fp32 MFMA
-    peak, algorithmic bytes / 8 TB/s), algorithmic bytes being every input
-    read once and the output written once.  A last line summarises."""
+    TFLOP/s, and the fraction of the op's roofline max(FLOP / MFMA peak of
+    `dtype`, algorithmic bytes / 8 TB/s), algorithmic bytes being every
+    input read once and the output written once (bf16 inputs, fp32
+    output).  A last line summarises."""
     import numpy as np
 
     from xtc_amd.artifacts import list_operations
@@ -272,7 +273,7 @@ def _named_ops(steps: int, warmup_ms: float) -> int:
     fracs = []
     for idx, (op, name) in enumerate(list_operations()):
         dims = _operation_dims(op, name)
-        graph = build_graph(op, dims, "float32", name=name.lower())
+        graph = build_graph(op, dims, dtype, name=name.lower())
         backend = Backend(graph)
         module = backend.get_compiler(synchronize=False, schedule_policy="strict").compile(
             backend.get_scheduler().schedule())
@@ -282,9 +283,9 @@ def _named_ops(steps: int, warmup_ms: float) -> int:
         status = dev.module_symbol(module, f"{module.payload_name}_status")
         status.restype = ctypes.c_int
         rng = np.random.default_rng(idx)
-        d_in = [DeviceArray.from_numpy(rng.uniform(-1, 1, t.constant_shape).astype(np.float32), "float32", dev)
+        d_in = [DeviceArray.from_numpy(rng.uniform(-1, 1, t.constant_shape).astype(np.float32), t.constant_dtype, dev)
                 for t in graph.inputs_types]
-        d_out = [DeviceArray(t.constant_shape, "float32", dev) for t in graph.outputs_types]
+        d_out = [DeviceArray(t.constant_shape, t.constant_dtype, dev) for t in graph.outputs_types]
         cargs = [ctypes.c_void_p(d.data) for d in (*d_in, *d_out)]
         _warm(lambda: fn(*cargs), lambda: capi.check(L.xtc_hip_synchronize(), "synchronize"), 3, warmup_ms)
         capi.check(L.xtc_hip_event_record(e0, None), "event")
@@ -298,13 +299,13 @@ def _named_ops(steps: int, warmup_ms: float) -> int:
         capi.check(L.xtc_hip_event_elapsed_ms(e0, e1, ctypes.byref(ms)), "elapsed")
         us = ms.value * 1e3 / steps
         flops = 2 * int(np.prod(dims[:7] if op == "conv2d" else dims))
-        nbytes = 4 * sum(d.size for d in (*d_in, *d_out))
-        roof_us = max(flops / (PEAK_TFLOPS["float32"] * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+        nbytes = sum(d.nbytes for d in (*d_in, *d_out))
+        t_mfma, t_hbm = flops / (PEAK_TFLOPS[dtype] * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)
+        roof_us = max(t_mfma, t_hbm) * 1e6
         fracs.append(roof_us / us)
-        print(json.dumps({"named_op": name, "operator": op, "dims": dims, "us": round(us, 2),
+        print(json.dumps({"named_op": name, "operator": op, "dtype": dtype, "dims": dims, "us": round(us, 2),
                           "tflops": round(flops / us / 1e6, 2), "roofline_us": round(roof_us, 2),
-                          "bound": "mfma" if flops / (PEAK_TFLOPS["float32"] * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9)
-                          else "hbm", "frac_of_roofline": round(roof_us / us, 4),
+                          "bound": "mfma" if t_mfma >= t_hbm else "hbm", "frac_of_roofline": round(roof_us / us, 4),
                           "kernel": "; ".join(f"{n}: {c.describe()}" for n, c in module.configs.items())}),
               flush=True)
         for d in (*d_in, *d_out):
@@ -367,7 +368,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--vs-hipblaslt", action="store_true",
                     help="also time torch.matmul on the same inputs (matmul configs) and report it in config")
     ap.add_argument("--named-ops", action="store_true",
-                    help="time every named operation of loop-explore --op-name with its default schedule (fp32)")
+                    help="time every named operation of loop-explore --op-name with its default schedule")
+    ap.add_argument("--named-dtype", default="float32", choices=["float32", "bfloat16"],
+                    help="operand type of --named-ops (bfloat16: fp32 accumulation and output)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch only the 1 GiB copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args(argv)
@@ -378,7 +381,7 @@ def main(argv: list[str] | None = None) -> int:
     if args.elementwise:
         return _elementwise(args.steps)
     if args.named_ops:
-        return _named_ops(args.steps, args.warmup_ms)
+        return _named_ops(args.steps, args.warmup_ms, args.named_dtype)
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU; a GEMM "

@@ -683,6 +683,13 @@ def test_instances_and_default_tile():
         ("float32", False, 512, 512, 512): ((64, 64, 32, 2, 2), 4),        # 64 tiles, 4 slabs per split
         ("float32", False, 128, 4096, 8192): ((64, 64, 32, 2, 2), 8),      # Llama3_QK: 128 tiles
         ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 1),     # 1152 tiles
+        # bf16: ping-pong from 128 aligned 256x256 tiles, else 128x128x64 (split-K to 512
+        # workgroups when that reaches 256), else the 64x64 rules
+        ("bfloat16", False, 3072, 24576, 3072): ((256, 256, 32, 2, 4), 1),
+        ("bfloat16", False, 2048, 4096, 256): ((256, 256, 32, 2, 4), 1),
+        ("bfloat16", False, 256, 8192, 4608): ((128, 128, 64, 2, 2), 4),
+        ("bfloat16", False, 2000, 2304, 2600): ((128, 128, 64, 2, 2), 1),
+        ("bfloat16", False, 1000, 1104, 1200): ((64, 64, 64, 2, 2), 1),
     }
     for args, (tile, split) in cases.items():
         got = capi.default_tile(*args)

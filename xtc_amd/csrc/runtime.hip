@@ -614,10 +614,30 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
     *split_k = s;
     return;
   }
-  if (!f32 && M >= 4096 && N >= 4096) {
-    // aligned shapes take the ping-pong LDS-DMA kernel behind this tile
-    if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && pick(256, 256, 32, 2, 4)) return;
-    if (pick(256, 256, 64, 2, 2)) return;
+  if (!f32 && !conv && M >= 128 && N >= 128) {
+    // bf16 matmuls, measured on MI355X over the op-name layers:
+    //  * aligned shapes with at least 128 256x256 tiles take the ping-pong
+    //    LDS-DMA kernel behind 256x256x32 (Gemma7B_FC 3072x24576x3072:
+    //    797 -> 406 us against 128x128x64; Gemma7B_In, K 256: 32.8 -> 19.3 us);
+    //  * the rest take 128x128x64 (Polybench_extralarge 2000x2304x2600:
+    //    68 us, against 98 us at 64x64x64 and 274 us at 256x256x64), with
+    //    fewer than 256 tiles split K up to 512 workgroups, at least 4 slabs
+    //    per split (Gemma27B_QKV 256x8192x4608: 85 -> 43 us at split 4),
+    //    when that makes at least 256 workgroups; smaller grids keep the
+    //    64x64 tiles below (Polybench_large 1000x1104x1200, whose K splits
+    //    into no whole slabs: 23 us at 64x64x64, 34 us on 72 128x128 tiles)
+    if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && (int64_t)(M / 256) * (N / 256) >= 128 &&
+        pick(256, 256, 32, 2, 4))
+      return;
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    int s = 1;
+    while (tiles < 256 && s < 32 && tiles * s * 2 <= 512 && K % (2 * s) == 0 && (K / (2 * s)) % 64 == 0 &&
+           K / (2 * s) >= 4 * 64)
+      s *= 2;
+    if (tiles * s >= 256 && pick(128, 128, 64, 2, 2)) {
+      *split_k = s;
+      return;
+    }
   }
   // large aligned fp32 shapes with at least one 256x128 tile per CU: the
   // LDS-DMA fp32 kernel behind this tile
