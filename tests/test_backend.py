@@ -690,6 +690,17 @@ def test_instances_and_default_tile():
         ("bfloat16", False, 256, 8192, 4608): ((128, 128, 64, 2, 2), 4),
         ("bfloat16", False, 2000, 2304, 2600): ((128, 128, 64, 2, 2), 1),
         ("bfloat16", False, 1000, 1104, 1200): ((64, 64, 64, 2, 2), 1),
+        # bf16 convs: 128x128x64 from 256 such tiles over >= 96 filters; a split of
+        # 4 or more moves to 128x64x64 when that still makes >= 256 workgroups
+        ("bfloat16", True, 289, 28272, 1024): ((128, 128, 64, 2, 2), 1),     # Yolo9000_23
+        ("bfloat16", True, 224 * 224, 96, 147): ((128, 128, 64, 2, 2), 1),   # SqueezeNet_00
+        ("bfloat16", True, 136 * 136, 128, 576): ((64, 64, 64, 2, 2), 1),    # Yolo9000_04: 145 such tiles
+        ("bfloat16", True, 272 * 272, 64, 288): ((64, 64, 64, 2, 2), 1),     # Yolo9000_02: 64 filters
+        ("bfloat16", True, 34 * 34, 512, 2304): ((128, 64, 64, 2, 2), 4),    # Yolo9000_12
+        ("bfloat16", True, 17 * 17, 1024, 4608): ((128, 64, 64, 2, 2), 8),   # Yolo9000_18
+        ("bfloat16", True, 49, 512, 4608): ((64, 64, 64, 2, 2), 8),          # ResNet18_12: 49 pixels
+        ("bfloat16", True, 28 * 28, 256, 2304): ((64, 64, 64, 2, 2), 4),     # MobilNet_05: 112 workgroups
+        ("bfloat16", True, 17 * 17, 512, 1024): ((64, 64, 64, 2, 2), 4),     # Yolo9000_19: 96 workgroups
     }
     for args, (tile, split) in cases.items():
         got = capi.default_tile(*args)

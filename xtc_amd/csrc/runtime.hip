@@ -647,8 +647,24 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   if (M >= 2048 && N >= 2048) {
     if (pick(128, 128, bk, 2, 2)) return;
   }
+  if (!f32 && conv && N >= 96 && (int64_t)((M + 127) / 128) * ((N + 127) / 128) >= 256 && pick(128, 128, 64, 2, 2))
+    // bf16 convs with at least 256 128x128 tiles over 96 filters or more
+    // (measured on MI355X: Yolo9000_23 1x1, 289 x 28272 x 1024: 86.7 -> 78.3
+    // us against 64x64x64; SqueezeNet_00 7x7/2 over 96 filters: 39.2 -> 36.2
+    // us; narrower convs lose with the half-empty 128-wide tile)
+    return;
   if (pick(64, 64, bk, 2, 2)) {
     fill(conv ? 256 : 512);
+    // bf16 convs that split K four ways or more and still make at least
+    // 256 workgroups of 128x64 tiles: the same split on those tiles
+    // (Yolo9000_12 3x3, 1156 x 512 x 2304, split 4, 320 workgroups: 31.3
+    // -> 26.4 us; Yolo9000_18, 289 x 1024 x 4608, split 8, 384: 31.5 ->
+    // 27.3 us).  Smaller grids lose (MobilNet_05, 112 workgroups: 18.1 ->
+    // 24.4 us; Yolo9000_19, 96: 12.4 -> 16.6 us), and so do the mostly
+    // empty 128-row tiles under 128 pixels (ResNet18_12: 17.6 -> 20.2 us)
+    if (!f32 && conv && M >= 128 && *split_k >= 4 &&
+        (int64_t)((M + 127) / 128) * ((N + 63) / 64) * *split_k >= 256)
+      pick(128, 64, 64, 2, 2);
     return;
   }
   int n = 0;
