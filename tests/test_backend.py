@@ -699,8 +699,15 @@ def test_instances_and_default_tile():
         ("bfloat16", True, 34 * 34, 512, 2304): ((128, 64, 64, 2, 2), 4),    # Yolo9000_12
         ("bfloat16", True, 17 * 17, 1024, 4608): ((128, 64, 64, 2, 2), 8),   # Yolo9000_18
         ("bfloat16", True, 49, 512, 4608): ((64, 64, 64, 2, 2), 8),          # ResNet18_12: 49 pixels
-        ("bfloat16", True, 28 * 28, 256, 2304): ((64, 64, 64, 2, 2), 4),     # MobilNet_05: 112 workgroups
+        ("bfloat16", True, 28 * 28, 256, 2304): ((64, 64, 64, 2, 2), 8),     # MobilNet_05: 224 workgroups
         ("bfloat16", True, 17 * 17, 512, 1024): ((64, 64, 64, 2, 2), 4),     # Yolo9000_19: 96 workgroups
+        # bf16 convs split K unequally up to 8 when the slabs do not divide
+        ("bfloat16", True, 15 * 15, 384, 1728): ((64, 64, 64, 2, 2), 4),     # AlexNet_02: 27 slabs
+        ("bfloat16", True, 15 * 15, 256, 3456): ((64, 64, 64, 2, 2), 8),     # AlexNet_03
+        ("bfloat16", True, 56 * 56, 64, 576): ((64, 64, 64, 2, 2), 2),       # ResNet18_02: 9 slabs
+        ("bfloat16", True, 14 * 14, 512, 4608): ((64, 64, 64, 2, 2), 8),     # MobilNet_07: 16 needs whole slabs
+        ("bfloat16", True, 7 * 7, 1024, 9216): ((64, 64, 64, 2, 2), 16),     # MobilNet_09: whole slabs
+        ("float32", True, 56 * 56, 64, 576): ((64, 64, 16, 2, 2), 4),        # fp32: whole slabs (8 would be 4.5)
     }
     for args, (tile, split) in cases.items():
         got = capi.default_tile(*args)

@@ -574,12 +574,18 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   // 512^3 fp32 19 -> 13 us; Yolo9000_09 (146 tiles, K 256) lost 7-12 % at
   // split 2 or 4 against its direct conv, and shapes with more tiles gain
   // little or lose (C4's 392 tiles keep the direct conv).
+  // bf16 convs also split into unequal parts (the last split shorter) up
+  // to 8: their K = R*S*C rarely splits into whole 64-deep slabs (AlexNet_02
+  // 3x3x192: 35.4 us at split 1 -> 15.0 us at split 4; AlexNet_03 36.1 ->
+  // 16.2 us at 8; ResNet18_02 15.2 -> 12.8 us at 2).  Beyond 8 the unequal
+  // splits gain nothing (MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16).
+  const bool ragged = conv && !f32;
   auto fill = [&](int64_t below) {
     const int64_t tiles = (int64_t)((M + t->bm - 1) / t->bm) * ((N + t->bn - 1) / t->bn);
     if (tiles >= below || (tiles >= 128 && K < 512)) return;
     int s = 1;
-    while (s < 32 && tiles * s * 2 <= 1024 && K % (2 * s) == 0 && (K / (2 * s)) % t->bk == 0 &&
-           K / (2 * s) >= 4 * t->bk)
+    while (s < 32 && tiles * s * 2 <= 1024 && K / (2 * s) >= 4 * t->bk &&
+           ((K % (2 * s) == 0 && (K / (2 * s)) % t->bk == 0) || (ragged && 2 * s <= 8)))
       s *= 2;
     *split_k = s;
   };
