@@ -707,11 +707,31 @@ def test_instances_and_default_tile():
         ("bfloat16", True, 56 * 56, 64, 576): ((64, 64, 64, 2, 2), 2),       # ResNet18_02: 9 slabs
         ("bfloat16", True, 14 * 14, 512, 4608): ((64, 64, 64, 2, 2), 8),     # MobilNet_07: 16 needs whole slabs
         ("bfloat16", True, 7 * 7, 1024, 9216): ((64, 64, 64, 2, 2), 16),     # MobilNet_09: whole slabs
-        ("float32", True, 56 * 56, 64, 576): ((64, 64, 16, 2, 2), 4),        # fp32: whole slabs (8 would be 4.5)
+        ("float32", True, 56 * 56, 64, 576): ((64, 64, 16, 2, 2), 8),        # ResNet18_02: 36 slabs, 8 unequal
+        ("float32", True, 15 * 15, 384, 1728): ((64, 64, 16, 2, 2), 8),      # fp32 AlexNet_02: unequal split 8
+        ("float32", True, 27 * 27, 192, 432): ((64, 64, 16, 2, 2), 4),       # SqueezeNet_13: K % 64 != 0
+        ("float32", True, 27 * 27, 32, 256): ((64, 64, 16, 2, 2), 4),        # SqueezeNet_08: 32 filters
+        ("float32", True, 112 * 112, 32, 288): ((64, 64, 32, 2, 2), 1),      # MobilNet_01: no split
+        ("float32", True, 272 * 272, 64, 288): ((64, 64, 32, 2, 2), 1),     # Yolo9000_02: no split
     }
     for args, (tile, split) in cases.items():
         got = capi.default_tile(*args)
         assert (tuple(got[0]), got[1]) == (tile, split), (args, got)
+
+
+def test_conv_default_tile_direct_block():
+    # the 8x14 direct conv block replaces the 8x8 one for windows wider than
+    # 1x1 whose 8x14 blocks fit in one wave of 256 CUs
+    def tile(n, h, w, c, f, r, pad):
+        d = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=n, H=h, W=w, C=c, F=f, R=r, S=r, stride_h=1, stride_w=1,
+                            pad_top=pad, pad_bottom=pad, pad_left=pad, pad_right=pad)
+        return capi.conv2d_default_tile(d)[0]
+
+    assert tile(8, 56, 56, 64, 64, 3, 1) == (112, 64, 16, 1, 4)      # C4: 224 blocks
+    assert tile(1, 70, 70, 128, 256, 3, 0) == (112, 64, 16, 1, 4)    # Yolo9000_08: 180 blocks
+    assert tile(1, 138, 138, 64, 128, 3, 0) == (64, 64, 16, 2, 2)    # Yolo9000_04: 340 blocks
+    assert tile(1, 68, 68, 256, 128, 1, 0) == (64, 64, 16, 2, 2)     # Yolo9000_09: 1x1
+    assert tile(1, 56, 56, 64, 64, 1, 0) == (64, 64, 16, 2, 2)       # ResNet18_03: 1x1
 
 
 def test_datasheet_flops_are_half_the_flop_rate():

@@ -574,12 +574,13 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   // 512^3 fp32 19 -> 13 us; Yolo9000_09 (146 tiles, K 256) lost 7-12 % at
   // split 2 or 4 against its direct conv, and shapes with more tiles gain
   // little or lose (C4's 392 tiles keep the direct conv).
-  // bf16 convs also split into unequal parts (the last split shorter) up
-  // to 8: their K = R*S*C rarely splits into whole 64-deep slabs (AlexNet_02
-  // 3x3x192: 35.4 us at split 1 -> 15.0 us at split 4; AlexNet_03 36.1 ->
-  // 16.2 us at 8; ResNet18_02 15.2 -> 12.8 us at 2).  Beyond 8 the unequal
-  // splits gain nothing (MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16).
-  const bool ragged = conv && !f32;
+  // Convs also split into unequal parts (the last split shorter) up to 8:
+  // their K = R*S*C rarely splits into whole slabs (bf16 AlexNet_02 3x3x192,
+  // 27 64-deep slabs: 35.4 us at split 1 -> 15.0 us at split 4; AlexNet_03
+  // 36.1 -> 16.2 us at 8; ResNet18_02 15.2 -> 12.8 us at 2; fp32 AlexNet_02
+  // 26.7 us at split 4 -> 18.4 us at 8).  Beyond 8 the unequal splits gain
+  // nothing (bf16 MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16).
+  const bool ragged = conv;
   auto fill = [&](int64_t below) {
     const int64_t tiles = (int64_t)((M + t->bm - 1) / t->bm) * ((N + t->bn - 1) / t->bn);
     if (tiles >= below || (tiles >= 128 && K < 512)) return;
@@ -592,6 +593,15 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   if (conv && f32 && N % 64 == 0 && K % 64 == 0 && pick(64, 64, 16, 2, 2)) {
     fill(256);
     return;
+  }
+  // other fp32 convs: 64x64x16 when its fill rule splits K (SqueezeNet_13
+  // 3x3x48, 36 tiles: 23.0 us on 64x64x32 -> 12.2 us at split 4;
+  // SqueezeNet_08/14 1x1, 12 tiles: 11.4/13.9 -> 9.8/11.1 us), else the
+  // 64x64x32 tile below, which wins unsplit (Yolo9000_02: 41.8 us against
+  // 48.2 on 64x64x16)
+  if (conv && f32 && pick(64, 64, 16, 2, 2)) {
+    fill(256);
+    if (*split_k > 1) return;
   }
   if (M <= 16) {
     // skinny bf16 with aligned N and K: the B-streaming kernel
@@ -1032,14 +1042,20 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int 
 
 // The tile a conv2d descriptor gets when it leaves `tile` zeroed: the shape
 // class default of default_tile, upgraded from the 8x8 direct conv block to
-// the 8x14 one (one block per CU for 8x56x56 outputs; 6 % faster on C4 in one
-// process) when the direct kernel takes the shape with it.
+// the 8x14 one when the direct kernel takes the shape with it, the window is
+// wider than 1x1 (the 8x14 block shares more of the input halo) and its
+// blocks fit in one wave over the chip's 256 CUs.  Measured on MI355X: C4
+// (8x56x56, 3x3, 224 blocks) 26.8 -> 23.0 us; Yolo9000_08 (68x68, 3x3, 180
+// blocks) 47.6 -> 41.3 us; but Yolo9000_04 (340 blocks) 39.8 -> 41.4 us, and
+// the 1x1 convs lose (Yolo9000_09 10.6 -> 15.6 us, ResNet18_03 5.0 -> 6.8).
 void default_conv_tile(const xtc_hip_conv2d_desc& d, int OH, int OW, xtc_hip_tile* t, int* split_k) {
   default_tile(d.dtype, 1, d.N * OH * OW, d.F, d.R * d.S * d.C, t, split_k);
   const xtc_hip_tile wide{112, 64, 16, 1, 4};
+  const DirectConvTile* dw = direct_conv_tile(wide);
   const void* p = (const void*)(uintptr_t)256;
-  if (same_tile(*t, xtc_hip_tile{64, 64, 16, 2, 2}) && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr))
-    *t = wide;
+  if (!dw || d.R * d.S == 1 || !same_tile(*t, xtc_hip_tile{64, 64, 16, 2, 2})) return;
+  const int64_t blocks = (int64_t)d.N * ((OH + dw->th - 1) / dw->th) * ((OW + dw->tw - 1) / dw->tw) * (d.F / dconv::FB);
+  if (blocks <= 256 && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr)) *t = wide;
 }
 
 int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int stages, int lda, int ldb,
