@@ -681,7 +681,12 @@ def test_instances_and_default_tile():
         ("float32", True, 68 * 68, 128, 256): ((64, 64, 16, 2, 2), 1),     # Yolo9000_09: 146 tiles, K 256
         ("float32", True, 112 * 112, 64, 576): ((64, 64, 16, 2, 2), 4),    # MobilNet_02: 196 tiles
         ("float32", False, 512, 512, 512): ((64, 64, 32, 2, 2), 4),        # 64 tiles, 4 slabs per split
-        ("float32", False, 128, 4096, 8192): ((64, 64, 32, 2, 2), 8),      # Llama3_QK: 128 tiles
+        ("float32", False, 128, 4096, 8192): ((128, 128, 32, 2, 4), 8),    # Llama3_QK: LDS-DMA fp32, 256 WGs
+        ("float32", False, 256, 8192, 4608): ((128, 128, 32, 2, 4), 2),    # Gemma27B_QKV: 128 tiles
+        ("float32", False, 256, 3584, 8192): ((128, 128, 32, 2, 4), 4),    # Gemma9B_QK: 224 WGs
+        ("float32", False, 256, 3072, 8192): ((64, 64, 32, 2, 2), 4),      # Gemma7B_QK: 192 would idle CUs
+        ("float32", False, 128, 4096, 8000): ((64, 64, 32, 2, 2), 8),      # unaligned K: 64x64 split-K
+        ("float32", False, 1000, 1104, 1200): ((64, 64, 32, 2, 2), 2),     # Polybench_large: unequal split
         ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 1),     # 1152 tiles
         # bf16: ping-pong from 128 aligned 256x256 tiles, else 128x128x64 (split-K to 512
         # workgroups when that reaches 256), else the 64x64 rules
