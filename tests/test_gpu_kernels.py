@@ -623,6 +623,30 @@ def test_pingpong_bf16_transposed_b_matches_row_major_and_bk64():
     np.testing.assert_array_equal(out, same)
 
 
+@needs_specialised
+def test_pingpong_bf16_split_k_bias_relu_strided():
+    # split-K runs on the ping-pong kernel itself (its pipeline depths 3-5,
+    # not the generic template's) when K splits into equal whole slabs: the
+    # last workgroup of each tile sums the partial planes with bias and relu
+    M, N, K = 512, 768, 1536
+    d = capi.MatmulDesc(dtype=capi.XTC_HIP_BF16, M=M, N=N, K=K, tile=capi.Tile(*PINGPONG), split_k=3)
+    assert sorted(capi.matmul_pipeline_depths(d)) == [3, 4, 5]
+    a, b = _int_operands(M, N, K, 7)
+    bias = np.arange(-(N // 2), N - N // 2, dtype=np.float32)
+    for split in (2, 3, 6):
+        out = _run_strided(a, b, PINGPONG, lda=K + 64, ldb=N + 256, ldc=N + 4, relu=True, bias=bias, split_k=split)
+        np.testing.assert_array_equal(out, ref.relu(ref.matmul(a, b) + bias).astype(np.float32), err_msg=f"{split}")
+    rng = np.random.default_rng(29)
+    ar = ref.round_bf16(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    br = ref.round_bf16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    out = _run_strided(ar, br, PINGPONG, lda=K, ldb=N, ldc=N, split_k=4)
+    assert ref.scaled_error(out, ref.matmul(ar, br), K, 1.0, 1.0) <= TOL_BF16
+    # two launches in a row reuse the arrival counters: the second must not
+    # see the first's counts
+    again = _run_strided(ar, br, PINGPONG, lda=K, ldb=N, ldc=N, split_k=4)
+    np.testing.assert_array_equal(out, again)
+
+
 # ------------- LDS-DMA fp32 kernel (BK 32: 128x256, 256x128, 128x128; BK 16: 128x256, 256x128)
 
 F32_LDS = [(128, 256, 32, 2, 4), (256, 128, 32, 4, 2), (128, 128, 32, 2, 4), (128, 256, 16, 2, 4), (256, 128, 16, 4, 2)]
@@ -844,6 +868,10 @@ DEPTH_CASES = [
     ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 512, 160), False),
     ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 512, 1056), False),
     ("bfloat16", (256, 256, 32, 2, 4), 1, (512, 256, 224), True),
+    # ping-pong split-K: 16, 16 and 3 slabs per split (3 < the DMA lead)
+    ("bfloat16", (256, 256, 32, 2, 4), 2, (512, 512, 1024), False),
+    ("bfloat16", (256, 256, 32, 2, 4), 4, (256, 512, 2048), True),
+    ("bfloat16", (256, 256, 32, 2, 4), 8, (256, 256, 768), False),
     ("bfloat16", (16, 128, 64, 1, 4), 8, (16, 1024, 8192), False),
     ("bfloat16", (16, 128, 64, 1, 4), 8, (12, 1024, 4096), False),
     # split-wave register ring: 8 chunks per wave, then 3 and 5 (not multiples of the depth)

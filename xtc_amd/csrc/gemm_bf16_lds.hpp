@@ -60,6 +60,13 @@ struct BigGemmArgs {
   int tiles_m, tiles_n;
   int group_m;
   int xcd_remap;
+  // split-K (gemm_bf16_pingpong only): split blockIdx.z covers K range
+  // [z * k_per_split, (z + 1) * k_per_split); with more than one split the
+  // workgroups store fp32 partial sums in partial[splits][M][N] and the last
+  // to arrive at its tile's counter sums them into C (splitk.hpp)
+  int k_per_split;
+  float* partial;
+  unsigned* counters;
 };
 
 namespace big {

@@ -38,12 +38,20 @@
 // phase.  Accumulation order per output element is the K walk, as in
 // gemm_bf16_lds.hpp: results are bit-identical to it on exactly summable
 // inputs.
+//
+// Split-K: blockIdx.z picks a range of k_per_split (whole slabs, equal for
+// every split) and the walk above runs over it.  With more than one split
+// the epilogue stores the fp32 accumulators into the split's partial plane,
+// and the last workgroup to arrive at the tile's counter sums the planes in
+// split order into C with bias and relu (splitk.hpp), then resets the
+// counter for the next launch.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "gemm_bf16_lds.hpp"
 #include "lds_dma.hpp"
+#include "splitk.hpp"
 
 namespace xtc_hip {
 
@@ -121,10 +129,12 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_bf16
       b_off[i] = bk * args.ldb + ((slot >> 1) ^ swz_b(bk)) * 16 + (slot & 1) * 8;
     }
   }
-  const __bf16* a_base = args.A + (size_t)m0 * args.lda;
-  const __bf16* b_base = BT ? args.B + (size_t)n0 * args.ldb : args.B + n0;
+  const int split = blockIdx.z;
+  const int k_begin = split * args.k_per_split;
+  const __bf16* a_base = args.A + (size_t)m0 * args.lda + k_begin;
+  const __bf16* b_base = BT ? args.B + (size_t)n0 * args.ldb + k_begin : args.B + (size_t)k_begin * args.ldb + n0;
   const size_t b_step = BT ? (size_t)BK : (size_t)BK * args.ldb;
-  const int nk = args.K / BK;
+  const int nk = min(args.K - k_begin, args.k_per_split) / BK;
   // K-stagger: tile (tm, tn) starts its K walk at slab (tm + 2 tn) mod 16
   int kofs = (tile_m + 2 * tile_n) & 15;
   kofs = nk > 0 ? kofs % nk : 0;
@@ -199,6 +209,23 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(512, 512))) gemm_bf16
   // ---- epilogue: lane holds C[m][n .. n+3] for each (it, jt); rows in order
   const int mrow = m0 + wm * (16 * TM) + l16;
   const int ncol = n0 + wn * (16 * TN) + 4 * g;
+  if (gridDim.z > 1) {
+    float* plane = args.partial + (size_t)split * args.M * args.N;
+#pragma unroll
+    for (int it = 0; it < TM; ++it) {
+#pragma unroll
+      for (int jt = 0; jt < TN; ++jt) splitk_store4(plane + (size_t)(mrow + it * 16) * args.N + ncol + jt * 16, acc[it][jt]);
+    }
+    // the arrival flag takes the first word of stage 0: every wave's LDS
+    // reads and DMAs are complete before the barrier that opens the arrival
+    unsigned* counter = args.counters + tile_m * args.tiles_n + tile_n;
+    if (splitk_arrive_in(counter, (int)gridDim.z, reinterpret_cast<unsigned*>(st0))) {
+      splitk_finish_tile<BM, BN, 512>(args.partial, args.C, args.bias, args.M, args.N, args.ldc, (int)gridDim.z,
+                                      args.relu, args.relu_threshold, m0, n0);
+      splitk_release(counter);
+    }
+    return;
+  }
   f32x4 bv[TN];
 #pragma unroll
   for (int jt = 0; jt < TN; ++jt)

@@ -770,6 +770,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // waves (gemm_bf16_lds.hpp) and the 256x256x32 tile with 2x4 waves
 // (gemm_bf16_pingpong.hpp) when the shape needs no bounds checks, for B
 // row-major (bt = false, ldb >= N) or stored transposed (bt = true, ldb >= K).
+// The ping-pong kernel also splits K, into equal ranges of whole slabs.
 // XTC_HIP_GENERIC_GEMM=1 forces the generic template (for A/B comparisons).
 bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda,
                           int ldb, int ldc, const void* A, const void* B, const void* C,
@@ -778,7 +779,8 @@ bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
     const char* v = getenv("XTC_HIP_GENERIC_GEMM");
     return v && v[0] == '1';
   }();
-  if (disabled || d.dtype != XTC_HIP_BF16 || split_k > 1) return false;
+  const int splits = split_k < 1 ? 1 : split_k;
+  if (disabled || d.dtype != XTC_HIP_BF16 || (splits > 1 && t.bk != 32)) return false;
   if (t.bm != 256 || t.bn != 256) return false;
   // bk 64: gemm_bf16_lds.hpp with 2x4 or 4x2 waves; bk 32: gemm_bf16_pingpong.hpp, 2x4
   if (t.bk == 64) {
@@ -786,7 +788,7 @@ bool lds_dma_gemm_applies(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, i
   } else if (t.bk != 32 || t.wgm != 2 || t.wgn != 4) {
     return false;
   }
-  if (d.M % 256 || d.N % 256 || d.K % t.bk) return false;
+  if (d.M % 256 || d.N % 256 || d.K % (t.bk * splits)) return false;
   if (lda % 8 || ldb % 8 || ldc % 4) return false;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias))) return false;
   // element offsets of one tile row/column range must fit in 32 bits
@@ -1076,9 +1078,11 @@ void default_conv_tile(const xtc_hip_conv2d_desc& d, int OH, int OW, xtc_hip_til
   if (blocks <= 256 && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr)) *t = wide;
 }
 
-int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int stages, int lda, int ldb,
-                        int ldc, const void* A, const void* B, float* C, const float* bias,
-                        hipStream_t s, bool bt) {
+int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int stages, int lda,
+                        int ldb, int ldc, const void* A, const void* B, float* C, const float* bias, Scratch& x,
+                        bool bt) {
+  const hipStream_t s = x.s;
+  const int splits = split_k < 1 ? 1 : split_k;
   BigGemmArgs a;
   a.A = (const __bf16*)A;
   a.B = (const __bf16*)B;
@@ -1096,7 +1100,16 @@ int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int
   a.tiles_n = d.N / 256;
   a.group_m = d.group_m > 0 ? d.group_m : 8;  // 8 <= 16 at 8192^3, zero and random data
   a.xcd_remap = d.xcd_remap;
-  dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  a.k_per_split = d.K / splits;
+  a.partial = nullptr;
+  a.counters = nullptr;
+  if (splits > 1) {
+    a.partial = x.partials((size_t)splits * d.M * d.N * sizeof(float));
+    if (!a.partial) return 1;
+    a.counters = x.counters((size_t)a.tiles_m * a.tiles_n);
+    if (!a.counters) return 1;
+  }
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
   if (t.bk == 32) {  // 2x4 waves: the ping-pong schedule, 3-5 stages of 32 KB
     const int st = stages ? stages : 4;
     if (bt && st == 4)
@@ -1394,7 +1407,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   // in a staging buffer first (one HBM-bound transpose).
   if (tb && !ta && lds_dma_gemm_applies(d, t, split_k, lda, ldb, ldc, A, B, C, bias, true)) {
     if (check_depth(MatmulPath::LdsDmaBt, t, 0, d.stages)) return 1;
-    return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, true);
+    return launch_lds_dma_gemm(d, t, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x, true);
   }
   const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
   if (ta) {
@@ -1425,7 +1438,8 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     HIP_TRY(hipGetLastError());
     return 0;
   }
-  if (path == MatmulPath::LdsDma) return launch_lds_dma_gemm(d, t, d.stages, lda, ldb, ldc, A, B, C, bias, s, false);
+  if (path == MatmulPath::LdsDma)
+    return launch_lds_dma_gemm(d, t, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x, false);
   if (path == MatmulPath::Skinny) return launch_skinny_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x);
   if (path == MatmulPath::SplitWave)
     return launch_splitwave_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, s);

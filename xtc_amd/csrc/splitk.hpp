@@ -146,18 +146,23 @@ __device__ __forceinline__ float splitk_sum1(const float* p, size_t stride, int 
 }
 
 // Step 2: true in the last-arriving workgroup only.  Called by every thread
-// of the workgroup (1-D blocks) after its splitk_store calls.
-__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int splits) {
-  __shared__ unsigned s_last;
+// of the workgroup (1-D blocks) after its splitk_store calls.  `flag` is one
+// LDS word that no thread touches between the first barrier here and the
+// return (a kernel whose LDS is full passes a word of its own, free by then).
+__device__ __forceinline__ bool splitk_arrive_in(unsigned* counter, int splits, unsigned* flag) {
   __builtin_amdgcn_s_waitcnt(splitk::kWaitVm0);
   __syncthreads();
   if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     (unsigned)(splits - 1)
-                 ? 1u
-                 : 0u;
+    *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1)
+                ? 1u
+                : 0u;
   __syncthreads();
-  return s_last != 0;
+  return *flag != 0;
+}
+
+__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int splits) {
+  __shared__ unsigned s_last;
+  return splitk_arrive_in(counter, splits, &s_last);
 }
 
 // Ends the protocol in the last workgroup (after its reads of the partials).
