@@ -684,9 +684,13 @@ def test_instances_and_default_tile():
         ("float32", False, 128, 4096, 8192): ((128, 128, 32, 2, 4), 8),    # Llama3_QK: LDS-DMA fp32, 256 WGs
         ("float32", False, 256, 8192, 4608): ((128, 128, 32, 2, 4), 2),    # Gemma27B_QKV: 128 tiles
         ("float32", False, 256, 3584, 8192): ((128, 128, 32, 2, 4), 4),    # Gemma9B_QK: 224 WGs
-        ("float32", False, 256, 3072, 8192): ((64, 64, 32, 2, 2), 4),      # Gemma7B_QK: 192 would idle CUs
+        ("float32", False, 256, 3072, 8192): ((64, 64, 32, 2, 2), 8),      # Gemma7B_QK: 192 would idle CUs
         ("float32", False, 128, 4096, 8000): ((64, 64, 32, 2, 2), 8),      # unaligned K: 64x64 split-K
-        ("float32", False, 1000, 1104, 1200): ((64, 64, 32, 2, 2), 2),     # Polybench_large: unequal split
+        ("float32", False, 1000, 1104, 1200): ((64, 64, 32, 2, 2), 8),     # Polybench_large: unequal split
+        ("float32", False, 256, 4608, 8192): ((64, 64, 32, 2, 2), 8),      # Gemma27B_QK: 2304 workgroups
+        ("float32", False, 768, 768, 4096): ((64, 64, 32, 2, 2), 16),      # 144 tiles x 16
+        ("float32", False, 256, 1024, 4096): ((64, 64, 32, 2, 2), 16),     # LDS-DMA splits would be 256 deep
+        ("float32", False, 1024, 1024, 8192): ((128, 128, 32, 2, 4), 4),   # 64 tiles x 4, 2048 deep
         ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 1),     # 1152 tiles
         # bf16: ping-pong from 128 aligned 256x256 tiles, else 128x128x64 (split-K to 512
         # workgroups when that reaches 256), else the 64x64 rules

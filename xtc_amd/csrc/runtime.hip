@@ -580,12 +580,18 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   // 36.1 -> 16.2 us at 8; ResNet18_02 15.2 -> 12.8 us at 2; fp32 AlexNet_02
   // 26.7 us at split 4 -> 18.4 us at 8).  Beyond 8 the unequal splits gain
   // nothing (bf16 MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16).
+  // fp32 matmuls split up to 2304 workgroups, 9 per CU, and 16 splits
+  // (Gemma27B_QK 256x4608x8192, 288 tiles: 245 us at split 2, 185 us at
+  // split 8; 768x768x4096: 67 -> 57 us at split 16; Polybench_large 43 ->
+  // 42 us; 256x1024x4096: 30.4 us at split 16, 38.1 us at 32).
   const bool ragged = conv || f32;
+  const int64_t cap = f32 && !conv ? 2304 : 1024;
+  const int smax = f32 && !conv ? 16 : 32;
   auto fill = [&](int64_t below) {
     const int64_t tiles = (int64_t)((M + t->bm - 1) / t->bm) * ((N + t->bn - 1) / t->bn);
     if (tiles >= below || (tiles >= 128 && K < 512)) return;
     int s = 1;
-    while (s < 32 && tiles * s * 2 <= 1024 && K / (2 * s) >= 4 * t->bk &&
+    while (s < smax && tiles * s * 2 <= cap && K / (2 * s) >= 4 * t->bk &&
            ((K % (2 * s) == 0 && (K / (2 * s)) % t->bk == 0) || (ragged && 2 * s <= 8)))
       s *= 2;
     *split_k = s;
@@ -657,17 +663,19 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   }
   // aligned fp32 shapes with fewer than 256 128x128 tiles (the M = 128-256
   // projections): the LDS-DMA fp32 kernel behind 128x128x32, 2x4 waves,
-  // split K by powers of two to between 224 and 256 workgroups, one wave
-  // over the chip (Gemma27B_QKV 256x8192x4608, 128 tiles: 201 -> 154 us at
+  // split K by powers of two, at least 1024 deep each, to between 224 and
+  // 256 workgroups, one wave over the chip (Gemma27B_QKV 256x8192x4608, 128 tiles: 201 -> 154 us at
   // split 2; Gemma9B_QK 256x3584x8192, 56 tiles: 162 -> 138 us at split 4;
   // Llama3_QKV 86 -> 76 us).  Past 256 workgroups the second wave costs more
   // than the split gains (Gemma27B_QK, 72 tiles: 261 us at split 2, 264 us
   // at split 4), and 192 leave too many CUs idle (Gemma7B_QK, 48 tiles:
-  // 128 -> 138 us), so those keep the 64x64 split-K rule below.
+  // 128 -> 138 us), so those keep the 64x64 split-K rule below, as do
+  // shallow splits (256x1024x4096 at split 16, 256 deep: 36.7 us against
+  // 30.1 us on 64x64 tiles at split 8).
   if (f32 && !conv && M % 128 == 0 && N % 128 == 0 && K % 32 == 0) {
     const int64_t tiles = (int64_t)(M / 128) * (N / 128);
     int s = 1;
-    while (s < 32 && tiles * s * 2 <= 256 && K % (32 * s * 2) == 0 && K / (s * 2) >= 4 * 32) s *= 2;
+    while (s < 32 && tiles * s * 2 <= 256 && K % (32 * s * 2) == 0 && K / (s * 2) >= 1024) s *= 2;
     if (tiles < 256 && s > 1 && tiles * s >= 224 && pick(128, 128, 32, 2, 4)) {
       *split_k = s;
       return;
