@@ -574,12 +574,15 @@ void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int
   // 512^3 fp32 19 -> 13 us; Yolo9000_09 (146 tiles, K 256) lost 7-12 % at
   // split 2 or 4 against its direct conv, and shapes with more tiles gain
   // little or lose (C4's 392 tiles keep the direct conv).
-  // Convs also split into unequal parts (the last split shorter) up to 8:
-  // their K = R*S*C rarely splits into whole slabs (bf16 AlexNet_02 3x3x192,
+  // Convs and fp32 matmuls also split into unequal parts (the last split
+  // shorter) up to 8; a conv's K = R*S*C rarely splits into whole slabs
+  // (bf16 AlexNet_02 3x3x192,
   // 27 64-deep slabs: 35.4 us at split 1 -> 15.0 us at split 4; AlexNet_03
   // 36.1 -> 16.2 us at 8; ResNet18_02 15.2 -> 12.8 us at 2; fp32 AlexNet_02
-  // 26.7 us at split 4 -> 18.4 us at 8).  Beyond 8 the unequal splits gain
-  // nothing (bf16 MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16).
+  // 26.7 us at split 4 -> 18.4 us at 8; fp32 Polybench_large, 37.5 slabs
+  // of 32: 56.2 -> 42.2 us).  Beyond 8 the unequal splits gain nothing
+  // (bf16 MobilNet_07, K 4608: 18.6 us at 8, 19.2 at 16); bf16 matmuls
+  // keep whole slabs (Polybench_large: 22.4 us unsplit, 28.7 at split 2).
   // fp32 matmuls split up to 2304 workgroups, 9 per CU, and 16 splits
   // (Gemma27B_QK 256x4608x8192, 288 tiles: 245 us at split 2, 185 us at
   // split 8; 768x768x4096: 67 -> 57 us at split 16; Polybench_large 43 ->
