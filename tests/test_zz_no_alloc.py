@@ -97,6 +97,10 @@ CASES = [
     ("float32", (32, 32, 16, 1, 1), 4, (512, 512, 512), (256, 128, 256), {}),
     # ping-pong bf16 kernel, no split: scratch-free
     ("bfloat16", (256, 256, 32, 2, 4), 1, (1024, 1024, 1024), (512, 256, 512), {}),
+    # ping-pong bf16 kernel with split-K 4: partials and counters, relu and bias
+    ("bfloat16", (256, 256, 32, 2, 4), 4, (512, 768, 2048), (256, 256, 1024), {"relu": True, "bias": True}),
+    # ping-pong bf16 kernel reading B^T natively, split-K 2
+    ("bfloat16", (256, 256, 32, 2, 4), 2, (512, 512, 1024), (256, 512, 512), {"trans_b": True}),
 ]
 
 
