@@ -691,7 +691,9 @@ def test_instances_and_default_tile():
         ("float32", False, 768, 768, 4096): ((64, 64, 32, 2, 2), 16),      # 144 tiles x 16
         ("float32", False, 256, 1024, 4096): ((64, 64, 32, 2, 2), 16),     # LDS-DMA splits would be 256 deep
         ("float32", False, 1024, 1024, 8192): ((128, 128, 32, 2, 4), 4),   # 64 tiles x 4, 2048 deep
-        ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 1),     # 1152 tiles
+        ("float32", False, 2000, 2304, 2600): ((64, 64, 32, 2, 2), 2),     # 1152 tiles, K >= 2048: split 2
+        ("float32", False, 1536, 1536, 512): ((64, 64, 32, 2, 2), 1),      # 576 tiles over a short K
+        ("float32", False, 2000, 2400, 2600): ((64, 64, 32, 2, 2), 1),     # 1200 tiles: split 2 passes 2304
         # bf16: ping-pong from 128 aligned 256x256 tiles, else 128x128x64 (split-K to 512
         # workgroups when that reaches 256), else the 64x64 rules
         ("bfloat16", False, 3072, 24576, 3072): ((256, 256, 32, 2, 4), 1),
