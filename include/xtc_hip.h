@@ -206,6 +206,15 @@ int xtc_hip_pad(const float *x, float *y, int ndim, const int64_t *shape,
 int xtc_hip_cast_f32_to_bf16(const float *x, uint16_t *y, uint64_t n, void *stream);
 int xtc_hip_cast_bf16_to_f32(const uint16_t *x, float *y, uint64_t n, void *stream);
 
+/* sizeof(xtc_hip_matmul_desc) and sizeof(xtc_hip_conv2d_desc) as this library
+ * was compiled: a binding that declares the descriptors itself (ctypes, cgo)
+ * checks its own struct sizes against these before the first call, so a
+ * field it lacks fails loudly instead of being read past the end of its
+ * struct.  No counterpart in the reference, whose mgpu* calls
+ * (GPUDevice.py:131-207) take no structs. */
+int xtc_hip_matmul_desc_size(void);
+int xtc_hip_conv2d_desc_size(void);
+
 /* Compiled kernel instances.  A schedule maps onto one of these; the HIP
  * Scheduler rejects schedules that map to none. */
 typedef struct {

@@ -567,6 +567,49 @@ def test_pipeline_depth_queries():
         capi.matmul_pipeline_depths(d)
 
 
+def _conv_c(C, tile=None, split_k=0, pad_value=0.0):
+    c = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=8, H=56, W=56, C=C, F=64, R=3, S=3, stride_h=1, stride_w=1,
+                        pad_top=1, pad_bottom=1, pad_left=1, pad_right=1, pad_value=pad_value, split_k=split_k)
+    if tile:
+        c.tile = capi.Tile(*tile)
+    return c
+
+
+def test_conv_pipeline_depths_describe_the_channel_staged_kernel():
+    # C = 3 is copied with a zero channel up to C = 4 and runs the MFMA conv:
+    # the depth query answers for that kernel, exactly as for C = 4
+    for tile, sk in ((None, 0), ((64, 64, 16, 2, 2), 4), ((64, 64, 16, 2, 2), 1)):
+        assert capi.conv2d_pipeline_depths(_conv_c(3, tile, sk)) == capi.conv2d_pipeline_depths(_conv_c(4, tile, sk))
+    assert capi.conv2d_pipeline_depths(_conv_c(3, (64, 64, 16, 2, 2), 4)) == [4]  # register ring under split-K
+    # the direct-only tile needs 64-channel multiples: not runnable at C = 3 or 4
+    for C in (3, 4):
+        with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
+            capi.conv2d_pipeline_depths(_conv_c(C, (112, 64, 16, 1, 4)))
+    assert capi.conv2d_pipeline_depths(_conv_c(64, (112, 64, 16, 1, 4))) == [3]
+    # a non-finite pad value cannot be staged (inf * 0 is NaN): the scalar kernel
+    assert capi.conv2d_pipeline_depths(_conv_c(3, pad_value=float("inf"))) == [1]
+
+
+def _integration_structs():
+    """The ctypes structs of the binding INTEGRATION.md tells maintainers to write."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    block = re.search(r"```python\n(import ctypes\n\nclass Tile.*?)\nlib = ctypes\.CDLL", text, re.S)
+    assert block, "INTEGRATION.md: ctypes binding snippet not found"
+    ns: dict = {}
+    exec(compile(block.group(1), "INTEGRATION.md", "exec"), ns)
+    return ns
+
+
+def test_descriptor_sizes_match_the_library_and_the_documented_binding():
+    lib = capi.lib()  # loading checks capi's own structs against the library
+    assert ctypes.sizeof(capi.MatmulDesc) == lib.xtc_hip_matmul_desc_size()
+    assert ctypes.sizeof(capi.Conv2dDesc) == lib.xtc_hip_conv2d_desc_size()
+    ns = _integration_structs()
+    assert ctypes.sizeof(ns["MatmulDesc"]) == lib.xtc_hip_matmul_desc_size()
+    assert [f[0] for f in ns["MatmulDesc"]._fields_] == [f[0] for f in capi.MatmulDesc._fields_]
+    assert [f[0] for f in ns["Tile"]._fields_] == [f[0] for f in capi.Tile._fields_]
+
+
 def test_mapping_column_major_raster():
     g = _matmul(4096, 4096, 4096)
     attrs, s = _sched(g, {"i": {"i1": 128}, "j": {"j1": 128}, "k": {"k1": 16}}, order=["j", "i", "k", "i1", "j1", "k1"])
@@ -752,6 +795,26 @@ def test_datasheet_flops_are_half_the_flop_rate():
     assert lib.xtc_hip_datasheet_flops(b"int4") == 0.0
     # the measured peak needs a device: without one it reports an error
     assert lib.xtc_hip_evaluate_flops(b"float32") == 0.0 and "xtc_hip_init" in capi.last_error()
+    # a dtype with no MFMA peak reports 0.0 through the device interface, as the
+    # explorer's peak_time expects, without touching a device
+    from xtc_amd.runtimes.hip.device import HipDevice
+
+    assert HipDevice().evaluate_flops("int4") == 0.0
+
+
+def test_compile_service_refuses_to_start_after_the_gpu(monkeypatch):
+    from xtc_amd.backends.hip import compiler
+
+    class _Lib:
+        @staticmethod
+        def xtc_hip_stream():
+            return 0x1234  # a library stream exists: xtc_hip_init has run
+
+    monkeypatch.setattr(compiler.CompileService, "_server_started", False)
+    monkeypatch.setattr(compiler.capi, "lib", lambda: _Lib)
+    monkeypatch.setattr(compiler.capi, "library_available", lambda: True)
+    with pytest.raises(RuntimeError, match="start_server"):
+        compiler.CompileService(1)
 
 
 def test_device_count_without_gpu_is_safe():

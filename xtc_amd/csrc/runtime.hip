@@ -82,6 +82,10 @@ struct DeviceState {
   // last sequence number queued for it (xtc_hip_synchronize)
   unsigned* done_flag = nullptr;
   std::atomic<unsigned> done_seq{0};
+  // taking a sequence number and queuing its store happen under this lock,
+  // so concurrent callers queue their stores in number order and the word
+  // only grows
+  std::mutex done_mutex;
   std::unordered_map<hipStream_t, StreamScratch> scratch;  // by launch stream
   std::string arch, name;
 };
@@ -1551,9 +1555,15 @@ int xtc_hip_synchronize(void) {
   // runtime's completion signal), which decides the time of short
   // synchronous payloads.  The spin asks the stream itself every 50 us, so
   // it also ends on completion without the store and on an error.
-  const unsigned seq = d->done_seq.fetch_add(1u) + 1u;
-  hipLaunchKernelGGL(stream_done_kernel, dim3(1), dim3(64), 0, d->stream, d->done_flag, seq);
-  if (hipGetLastError() != hipSuccess) {
+  unsigned seq;
+  hipError_t launched;
+  {
+    std::lock_guard<std::mutex> lock(d->done_mutex);
+    seq = d->done_seq.fetch_add(1u) + 1u;
+    hipLaunchKernelGGL(stream_done_kernel, dim3(1), dim3(64), 0, d->stream, d->done_flag, seq);
+    launched = hipGetLastError();
+  }
+  if (launched != hipSuccess) {
     HIP_TRY(hipStreamSynchronize(d->stream));
     return 0;
   }
@@ -1697,6 +1707,9 @@ int xtc_hip_event_destroy(void* event) {
   return 0;
 }
 
+int xtc_hip_matmul_desc_size(void) { return (int)sizeof(xtc_hip_matmul_desc); }
+int xtc_hip_conv2d_desc_size(void) { return (int)sizeof(xtc_hip_conv2d_desc); }
+
 int xtc_hip_gemm_instance_count(void) {
   int n = 0, m = 0;
   gemm_registry(&n);
@@ -1763,20 +1776,30 @@ int xtc_hip_matmul_pipeline_depths(const xtc_hip_matmul_desc* desc, int* depths,
 
 int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths, int max_depths) {
   if (!desc || !depths || max_depths < 1) return -fail("null argument");
-  const xtc_hip_conv2d_desc& d = *desc;
+  xtc_hip_conv2d_desc d = *desc;
   const int HP = d.H + d.pad_top + d.pad_bottom;
   const int WP = d.W + d.pad_left + d.pad_right;
   if (d.stride_h <= 0 || d.stride_w <= 0 || HP < d.R || WP < d.S) return -fail("bad conv2d descriptor");
   const int OH = (HP - d.R) / d.stride_h + 1;
   const int OW = (WP - d.S) / d.stride_w + 1;
   const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const bool padded = d.pad_top || d.pad_bottom || d.pad_left || d.pad_right;
+  if (d.C % vec && d.F % vec == 0 && (!padded || isfinite(d.pad_value))) {
+    // xtc_hip_conv2d stages such a conv with zero channels up to the next
+    // whole vector and runs the MFMA conv on the copies: describe that kernel
+    d.C = (d.C + vec - 1) / vec * vec;
+  }
   if (d.C % vec || d.F % vec) {
     depths[0] = 1;  // scalar kernel
     return 1;
   }
   xtc_hip_tile t = d.tile;
   int split_k = d.split_k;
-  if (t.bm == 0) default_conv_tile(d, OH, OW, &t, &split_k);
+  if (t.bm == 0) {
+    int sk = 1;
+    default_conv_tile(d, OH, OW, &t, &sk);
+    if (split_k <= 0) split_k = sk;
+  }
   const GemmEntry* e = find_entry(d.dtype, 1, t);
   if (!e)
     return -fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype, t.bm, t.bn, t.bk,

@@ -158,6 +158,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "xtc_hip_cast_f32_to_bf16": (_i, [_vp, _vp, _u64, _vp]),
     "xtc_hip_cast_bf16_to_f32": (_i, [_vp, _vp, _u64, _vp]),
+    "xtc_hip_matmul_desc_size": (_i, []),
+    "xtc_hip_conv2d_desc_size": (_i, []),
     "xtc_hip_gemm_instance_count": (_i, []),
     "xtc_hip_gemm_instance_get": (_i, [_i, ctypes.POINTER(GemmInstance)]),
     "xtc_hip_default_tile": (
@@ -218,6 +220,11 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = res
                 fn.argtypes = args
+            for struct, size_fn in ((MatmulDesc, handle.xtc_hip_matmul_desc_size),
+                                    (Conv2dDesc, handle.xtc_hip_conv2d_desc_size)):
+                if ctypes.sizeof(struct) != size_fn():
+                    raise HipError(f"{struct.__name__} is {ctypes.sizeof(struct)} bytes here but "
+                                   f"{size_fn()} in {LIB_PATH.name}: the binding and include/xtc_hip.h differ")
             _lib = handle
     return _lib
 

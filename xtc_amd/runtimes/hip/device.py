@@ -197,16 +197,28 @@ class HipDevice(AcceleratorDevice):
 
     OPERANDS = {"reference": 0, "zero": 1, "random": 2}
 
+    # measured peaks by (device, dtype, operands): the probe takes ~0.4 s
+    _peaks: dict[tuple[int, str, str], float] = {}
+
     def evaluate_flops(self, dtype_name: str | bytes, operands: str = "reference") -> float:
         """Measured MFMA peak of the device in FMA/s (one XTC op per FMA):
         a register-only MFMA loop, operands the reference's integers
-        1 + i % 127 (evaluate_flops.c:466-469), "zero" or "random"."""
+        1 + i % 127 (evaluate_flops.c:466-469), "zero" or "random".
+        Measured once per process for each (device, dtype, operands).  A
+        dtype the device has no MFMA probe for gives 0.0, as the reference's
+        interface does for an unknown dtype; a failed probe raises."""
         name = dtype_name.decode() if isinstance(dtype_name, bytes) else dtype_name
-        self.init_device()
+        key = (self._device, name, operands)
+        if key in self._peaks:
+            return self._peaks[key]
         L = capi.lib()
+        if L.xtc_hip_datasheet_flops(name.encode()) <= 0.0:
+            return 0.0
+        self.init_device()
         v = float(L.xtc_hip_evaluate_flops_operands(name.encode(), self.OPERANDS[operands]))
         if v <= 0.0:
             raise capi.HipError(capi.last_error() or f"evaluate_flops({name}) failed")
+        self._peaks[key] = v
         return v
 
     @staticmethod

@@ -19,7 +19,10 @@ Searches: "random", "exhaustive", "data", "default", and "iterative"
 The exploring process also runs the GPU, so it starts no process once its
 GPU runtime is up: the payloads' gcc runs in a CompileService (worker
 processes of a fork server started before any GPU work), and the manifest's
-`git rev-parse` runs before the first evaluation.
+`git rev-parse` runs before the first evaluation.  A Python caller that has
+already run GPU work in its process calls CompileService.start_server()
+before that work; otherwise Exploration(config)() on the HIP backend raises
+instead of forking from a process whose GPU runtime is up.
 
 With the HIP backend the strategy's samples are filtered to those that map
 exactly onto a compiled kernel instance (schedule_policy "strict"), so every

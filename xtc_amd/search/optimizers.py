@@ -127,7 +127,7 @@ class RandomForestOptimizer(Optimizer):
         for xi, yi in zip(x, y):
             if yi > self.best_y:
                 self.best_x, self.best_y = list(xi), float(yi)
-        self.history.append(f"trial: {len(self.X)} best_y: {self.best_y} y: {list(y)} last_beta: {self.last_beta}")
+        self.history.append(f"after {len(self.X)} points: best {self.best_y}, batch {list(y)}, ucb beta {self.last_beta}")
         if len(self.X) < self.update_first:
             return
         n = self.update_first + (len(self.X) - self.update_first) // self.update_period * self.update_period

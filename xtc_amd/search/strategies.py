@@ -743,20 +743,22 @@ class Strategies:
 
     @classmethod
     def resolve_name(cls, name: str) -> str:
-        seen: set[str] = set()
-        while name in cls._aliases:
-            if name in seen:
-                raise ValueError(f"strategy alias cycle involving: {name}")
-            seen.add(name)
-            name = cls._aliases[name]
-        return name
+        """Follows aliases to a registered name; an alias loop is an error."""
+        chain = [name]
+        while chain[-1] in cls._aliases:
+            target = cls._aliases[chain[-1]]
+            if target in chain:
+                raise ValueError(f"aliases loop without reaching a strategy: {' -> '.join(chain + [target])}")
+            chain.append(target)
+        return chain[-1]
 
     @classmethod
     def registration(cls, name: str) -> StrategyRegistration:
         resolved = cls.resolve_name(name)
-        if resolved not in cls._map:
-            raise ValueError(f"unknown strategy name: {resolved}")
-        return cls._map[resolved]
+        reg = cls._map.get(resolved)
+        if reg is None:
+            raise ValueError(f"no strategy is registered as {resolved!r} (known: {', '.join(sorted(cls._map))})")
+        return reg
 
     @classmethod
     def from_name(cls, name: str) -> type[Strategy]:
