@@ -16,9 +16,10 @@ every box of this pool has one GPU.
 
 The cpu_baseline leg times the C restatement of XTC's llvmir CPU backend
 (oracle/, OpenMP on this host's cores): auto-scheduled over 64 seeded samples
-of the reference's tile_oo strategy at 1024^3, then the best schedule timed
-once at the workload's GEMM shape, with the reference's own evaluate_perf
-harness when oracle/_ref is built.
+each of the reference's tile_pprprp_vr and tile_oo strategies, then the best
+schedule timed at the workload's GEMM shape with repeat 5 and min_repeat_ms
+100, with the reference's own evaluate_perf harness when oracle/_ref is
+built.
 """
 
 from __future__ import annotations
@@ -97,11 +98,15 @@ def _vendor_matmul(host_in: list[np.ndarray], dtype: str, steps: int, warmup: in
 
 def _cpu_baseline(cfg: str) -> dict:
     """Times the CPU restatement of XTC's llvmir backend (oracle/) on this
-    host: auto-scheduled at a 1024^3 sample over 64 seeded samples of the
-    reference's tile_oo strategy (each sample compiled as its own object) and
-    the restatement's 8 fixed tile variants, then the winner timed once at
-    the workload's own GEMM shape (C1, C2, C3a, C3b), or a 512/2048 sample of
-    it for the conv and MLP workloads."""
+    host, auto-scheduled as loop-explore would: 64 seeded samples each of the
+    reference's tile_pprprp_vr and tile_oo strategies (every sample compiled
+    as its own object) plus the restatement's 8 fixed tile_oo variants, timed
+    at 1024^3; the 8 fastest re-timed on the workload's N x K with 32 rows
+    per thread; the winner then timed at the
+    workload's own GEMM shape (C1, C2, C3a, C3b; a 512/2048 sample of it for
+    the conv and MLP workloads) under the reference's evaluate_perf protocol
+    with repeat 5 and min_repeat_ms 100 (evaluate_perf.c:63-125): min and
+    median per call over the repeats."""
     from oracle import cpu_baseline as cb
     from xtc_amd.utils.bf16 import round_to_bf16
 
@@ -113,24 +118,39 @@ def _cpu_baseline(cfg: str) -> dict:
         return round_to_bf16(x) if bf16 else x
 
     cores = cb.threads()
-    tune = 1024
-    sched, t_sched, tried = cb.autoschedule_tile_oo(tune, trials=64, seed=0, bf16=bf16, jobs=min(16, cores))
+    jobs = min(16, cores)
+    tune, trials = 1024, 64
+    cands: list[tuple[float, tuple[int, ...], str]] = []
+    for strat in ("tile_pprprp_vr", "tile_oo"):
+        cands += [(t, s, strat) for t, s in cb.autoschedule_strategy(strat, tune, trials=trials, seed=0, bf16=bf16,
+                                                                      jobs=jobs)]
     at, bt = draw((tune, tune)), draw((tune, tune))
-    variant, t_var = cb.autoschedule_matmul(at, bt, repeat=1, min_repeat_ms=20)
-    use_sched = t_sched <= t_var
+    for v, (ti, tk, tj) in enumerate(cb.variants()):
+        cands.append((cb.time_schedule((ti, tk, tj), at, bt, repeat=1, min_repeat_ms=20), (ti, tk, tj), "tile_oo fixed"))
+    cands.sort()
     shape = {"C1": (512, 512, 512), "C2": (4096, 4096, 4096), "C3a": (8192, 8192, 8192),
              "C3b": (16, 8192, 8192)}.get(cfg, (2048, 2048, 2048) if cfg == "C5" else (512, 512, 512))
     m, n, k = shape
+
+    def fits(s: tuple[int, ...]) -> bool:  # a pprprp schedule's i1/j1 extents must divide the shape
+        return len(s) == 3 or (m % s[0] == 0 and n % s[3] == 0)
+
+    # re-rank the 8 fastest on the workload's own N x K with fewer rows (32 per
+    # thread): the panel traffic of a deep K is what a 1024^3 sample misses
+    ms = min(m, 32 * cores)
+    a2, b2 = draw((ms, k)), draw((k, n))
+    finalists = sorted((cb.time_schedule(s, a2, b2, repeat=1, min_repeat_ms=50), s, how)
+                       for _, s, how in [c for c in cands if fits(c[1]) and ms % c[1][0] == 0][:8])
+    _, sched, strat = finalists[0]
     a, b = draw((m, k)), draw((k, n))
-    if use_sched:
-        t = cb.time_schedule(sched, a, b, repeat=1, number=1, min_repeat_ms=0)
-        how = f"tile_oo sample (i1, k1, j1)={sched}, best of {tried} seeded samples and 8 fixed variants at {tune}^3"
-    else:
-        t = cb.time_matmul(a, b, variant, repeat=1, min_repeat_ms=0)
-        how = (f"fixed variant (i1, k1, j1)={cb.variants()[variant]}, faster at {tune}^3 than the best of {tried} "
-               f"seeded tile_oo samples {sched}")
+    repeat, min_repeat_ms = 5, 100
+    times = cb.time_schedule_repeats(sched, a, b, repeat=repeat, number=1, min_repeat_ms=min_repeat_ms)
+    t_min, t_med = min(times), statistics.median(times)
+    names = ("i1", "i2", "i3", "j1", "j2", "j3", "k1") if len(sched) == 7 else ("i1", "k1", "j1")
+    how = (f"{strat} schedule {dict(zip(names, sched))}: fastest at {ms}x{n}x{k} of the 8 best at {tune}^3 among "
+           f"{trials} seeded tile_pprprp_vr samples, {trials} seeded tile_oo samples and 8 fixed tile_oo variants")
     harness = "reference evaluate_perf" if cb.ref_runtime() is not None else "evaluate_perf protocol (Python)"
-    value = 2 * m * n * k / t / 1e12
+    value = 2 * m * n * k / t_min / 1e12
     # the host's peak as the reference's explorer takes it: evaluate_flops's
     # single-core FMA/s (evaluate_flops.c:461-494) times the cores
     # (explore.py:619-625 divides the peak time by the threads)
@@ -142,11 +162,16 @@ def _cpu_baseline(cfg: str) -> dict:
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
+        "repeat": repeat,
+        "min_repeat_ms": min_repeat_ms,
+        "min_ms": round(t_min * 1e3, 3),
+        "median_ms": round(t_med * 1e3, 3),
+        "median_tflops": round(2 * m * n * k / t_med / 1e12, 4),
         **peak,
         "sample": (
             f"fp32 matmul {m}x{n}x{k} ({'the workload shape' if cfg in ('C1', 'C2', 'C3a', 'C3b') else 'a sample'}"
-            f"{', bf16-rounded inputs' if bf16 else ''}), XTC llvmir restatement in loop order i,k,j,i1,k1,j1, "
-            f"{how}; one call after a warm-up; OpenMP {cores} threads, {harness}, CPU: {cb.cpu_model()}"
+            f"{', bf16-rounded inputs' if bf16 else ''}), XTC llvmir restatement, {how}; value from the min of "
+            f"{repeat} repeats (min_repeat_ms {min_repeat_ms}); OpenMP {cores} threads, {harness}, CPU: {cb.cpu_model()}"
         ),
     }
 

@@ -59,7 +59,88 @@
     }                                                                                    \
   }
 
-#if defined(XTC_CPU_TI) && defined(XTC_CPU_TK) && defined(XTC_CPU_TJ)
+#if defined(XTC_CPU_PPRPRP)
+/* One sampled schedule of the reference's tile_pprprp strategies
+ * (src/xtc/search/strategies.py:772-826: order i, j, i1, j1, k, i2, j2, k1,
+ * i3, j3; i and j parallel, j3 vectorised, the inner tiles i3, k1, j3
+ * unrolled), built alone with its tile extents as compile-time constants:
+ * -DXTC_CPU_I1/I2/I3 (extents of the i1, i2, i3 tiles), J1/J2/J3, K1.  Loop
+ * i steps by I1 and i1 walks it by I2, i2 by I3, as XTC lowers tiles
+ * (MlirCompilerPasses.py:414-457); the two parallel outer loops form one
+ * OpenMP iteration space (scf.forall over both, convert-scf-to-openmp).
+ * The fill node (linalg.fill 0) runs over each (i, j) block before its
+ * accumulation.  The extents divide the matrix sizes, as the strategy
+ * samples divisors. */
+#define XI1 XTC_CPU_I1
+#define XI2 XTC_CPU_I2
+#define XI3 XTC_CPU_I3
+#define XJ1 XTC_CPU_J1
+#define XJ2 XTC_CPU_J2
+#define XJ3 XTC_CPU_J3
+#define XK1 XTC_CPU_K1
+
+static void matmul_sched(const float *restrict A, const float *restrict B, float *restrict C, int M, int N,
+                         int K) {
+  const int nbi = M / XI1, nbj = N / XJ1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int bi = 0; bi < nbi; ++bi) {
+    for (int bj = 0; bj < nbj; ++bj) {
+      const int i0 = bi * XI1, j0 = bj * XJ1;
+      for (int i = i0; i < i0 + XI1; ++i) memset(C + (int64_t)i * N + j0, 0, sizeof(float) * XJ1);
+      for (int i1 = i0; i1 < i0 + XI1; i1 += XI2) {
+        for (int j1 = j0; j1 < j0 + XJ1; j1 += XJ2) {
+          for (int k = 0; k < K; k += XK1) {
+            for (int i2 = i1; i2 < i1 + XI2; i2 += XI3) {
+              for (int j2 = j1; j2 < j1 + XJ2; j2 += XJ3) {
+                float acc[XI3][XJ3];
+#pragma GCC unroll 64
+                for (int i3 = 0; i3 < XI3; ++i3)
+#pragma omp simd
+                  for (int j3 = 0; j3 < XJ3; ++j3) acc[i3][j3] = C[(int64_t)(i2 + i3) * N + j2 + j3];
+#pragma GCC unroll 16
+                for (int k1 = 0; k1 < XK1; ++k1) {
+                  const float *restrict b = B + (int64_t)(k + k1) * N + j2;
+#pragma GCC unroll 64
+                  for (int i3 = 0; i3 < XI3; ++i3) {
+                    const float a = A[(int64_t)(i2 + i3) * K + k + k1];
+#pragma omp simd
+                    for (int j3 = 0; j3 < XJ3; ++j3) acc[i3][j3] += a * b[j3];
+                  }
+                }
+#pragma GCC unroll 64
+                for (int i3 = 0; i3 < XI3; ++i3)
+#pragma omp simd
+                  for (int j3 = 0; j3 < XJ3; ++j3) C[(int64_t)(i2 + i3) * N + j2 + j3] = acc[i3][j3];
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+static int g_sched_m, g_sched_n, g_sched_k;
+
+void xtc_cpu_sched_configure(int M, int N, int K) {
+  g_sched_m = M;
+  g_sched_n = N;
+  g_sched_k = K;
+}
+
+/* The scheduled matmul called like an XTC module: void f(A, B, C). */
+void xtc_cpu_sched_payload(void *A, void *B, void *C) {
+  matmul_sched((const float *)A, (const float *)B, (float *)C, g_sched_m, g_sched_n, g_sched_k);
+}
+
+int xtc_cpu_sched_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+#elif defined(XTC_CPU_TI) && defined(XTC_CPU_TK) && defined(XTC_CPU_TJ)
 /* One sampled schedule, built alone with its tile sizes as compile-time
  * constants (-DXTC_CPU_TI=.. -DXTC_CPU_TK=.. -DXTC_CPU_TJ=..), as the code
  * MLIR emits for one loop-explore sample: i1 = TI, k1 = TK, j1 = TJ of the

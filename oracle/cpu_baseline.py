@@ -32,6 +32,9 @@ __all__ = [
     "schedule_lib",
     "time_schedule",
     "autoschedule_tile_oo",
+    "autoschedule_strategy",
+    "time_schedule_repeats",
+    "pprprp_tiles",
     "threads",
     "matmul",
     "conv2d",
@@ -207,23 +210,35 @@ def time_matmul(a: np.ndarray, b: np.ndarray, variant: int, repeat: int = 3, min
     return time_call(lambda: lib.xtc_cpu_matmul(variant, pa, pb, pc, m, n, k), repeat, min_repeat_ms)
 
 
-_sched_libs: dict[tuple[int, int, int], ctypes.CDLL] = {}
+_sched_libs: dict[tuple[int, ...], ctypes.CDLL] = {}
 
 
-def schedule_lib(ti: int, tk: int, tj: int) -> ctypes.CDLL:
-    """The restatement built for one tile_oo schedule (i1, k1, j1) =
-    (ti, tk, tj), tiles as compile-time constants; cached per host."""
-    key = (ti, tk, tj)
+def _sched_defines(tiles: tuple[int, ...]) -> list[str]:
+    """Compile-time tile constants of one schedule: 3 extents are a tile_oo
+    schedule (i1, k1, j1); 7 are a tile_pprprp one (i1, i2, i3, j1, j2, j3, k1)."""
+    if len(tiles) == 3:
+        return [f"-DXTC_CPU_{n}={v}" for n, v in zip(("TI", "TK", "TJ"), tiles)]
+    if len(tiles) == 7:
+        return ["-DXTC_CPU_PPRPRP"] + [f"-DXTC_CPU_{n}={v}" for n, v in zip(("I1", "I2", "I3", "J1", "J2", "J3", "K1"),
+                                                                             tiles)]
+    raise ValueError(f"schedule tiles {tiles}: expected 3 (tile_oo) or 7 (tile_pprprp) extents")
+
+
+def schedule_lib(*tiles: int) -> ctypes.CDLL:
+    """The restatement built for one schedule, tiles as compile-time
+    constants (see _sched_defines); cached per host."""
+    key = tuple(int(t) for t in tiles)
     if key in _sched_libs:
         return _sched_libs[key]
     out_dir = HERE / "_build" / _host_key()
-    lib = out_dir / f"libxtc_cpu_sched_{ti}_{tk}_{tj}.so"
+    tag = ("pprprp_" if len(key) == 7 else "") + "_".join(map(str, key))
+    lib = out_dir / f"libxtc_cpu_sched_{tag}.so"
     if not lib.exists():
         out_dir.mkdir(parents=True, exist_ok=True)
         cc = os.environ.get("CC", "gcc")
         tmp = lib.with_suffix(f".so.tmp{os.getpid()}")
         cmd = [cc, "-O3", "-march=native", "-ffp-contract=fast", "-fopenmp", "-fPIC", "-std=c11", "-shared",
-               f"-DXTC_CPU_TI={ti}", f"-DXTC_CPU_TK={tk}", f"-DXTC_CPU_TJ={tj}", "-o", str(tmp), str(SRC)]
+               *_sched_defines(key), "-o", str(tmp), str(SRC)]
         subprocess.run(cmd, check=True, capture_output=True)
         os.replace(tmp, lib)
     handle = ctypes.CDLL(str(lib))
@@ -233,10 +248,11 @@ def schedule_lib(ti: int, tk: int, tj: int) -> ctypes.CDLL:
     return handle
 
 
-def time_schedule(tiles: tuple[int, int, int], a: np.ndarray, b: np.ndarray, repeat: int = 2, number: int = 1,
-                  min_repeat_ms: int = 50) -> float:
-    """Seconds per call of one compiled schedule (min over repeats), with the
-    reference's evaluate_perf when oracle/_ref is built."""
+def time_schedule_repeats(tiles: tuple[int, ...], a: np.ndarray, b: np.ndarray, repeat: int = 2, number: int = 1,
+                          min_repeat_ms: int = 50) -> list[float]:
+    """Seconds per call of one compiled schedule for each repeat, with the
+    reference's evaluate_perf when oracle/_ref is built (one warm-up call,
+    then per repeat calls doubling from `number` until min_repeat_ms)."""
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     m, k = a.shape
@@ -250,10 +266,41 @@ def time_schedule(tiles: tuple[int, int, int], a: np.ndarray, b: np.ndarray, rep
         results = (ctypes.c_double * repeat)()
         args = (ctypes.c_void_p * 3)(a.ctypes.data, b.ctypes.data, c.ctypes.data)
         ref.evaluate_perf(results, 0, None, repeat, number, min_repeat_ms, fn, args, 3)
-        return float(min(results))
+        return [float(x) for x in results]
     payload = lib.xtc_cpu_sched_payload
     payload.argtypes = [ctypes.c_void_p] * 3
-    return time_call(lambda: payload(a.ctypes.data, b.ctypes.data, c.ctypes.data), repeat, min_repeat_ms)
+    return [time_call(lambda: payload(a.ctypes.data, b.ctypes.data, c.ctypes.data), 1, min_repeat_ms)
+            for _ in range(repeat)]
+
+
+def time_schedule(tiles: tuple[int, ...], a: np.ndarray, b: np.ndarray, repeat: int = 2, number: int = 1,
+                  min_repeat_ms: int = 50) -> float:
+    """Seconds per call of one compiled schedule, min over repeats."""
+    return min(time_schedule_repeats(tiles, a, b, repeat, number, min_repeat_ms))
+
+
+class _TileRecorder:
+    """Scheduler stand-in that records the tile extents a strategy's
+    generate() asks for (the only calls the PRT strategies make that the
+    restatement needs; the loop order, parallel, vector and unroll choices
+    of a scheme are fixed by the scheme and built into cpu_backend.c)."""
+
+    def __init__(self) -> None:
+        self.tiles: dict[str, dict[str, int]] = {}
+
+    def tile(self, axis: str, tiles: dict[str, int], root: str = ".") -> None:
+        self.tiles[axis] = dict(tiles)
+
+    def __getattr__(self, name: str):  # interchange, parallelize, vectorize, unroll, ...
+        return lambda *a, **k: None
+
+
+def pprprp_tiles(strategy, sample) -> tuple[int, ...]:  # type: ignore[no-untyped-def]
+    """(i1, i2, i3, j1, j2, j3, k1) extents of a tile_pprprp* sample."""
+    rec = _TileRecorder()
+    strategy.generate(rec, sample)
+    t = rec.tiles
+    return (t["i"]["i1"], t["i"]["i2"], t["i"]["i3"], t["j"]["j1"], t["j"]["j2"], t["j"]["j3"], t["k"]["k1"])
 
 
 def autoschedule_tile_oo(n: int, trials: int = 64, seed: int = 0, bf16: bool = False,
@@ -286,6 +333,42 @@ def autoschedule_tile_oo(n: int, trials: int = 64, seed: int = 0, bf16: bool = F
     timed = [(time_schedule(t, a, b, repeat=1, min_repeat_ms=20), t) for t in tiles]
     t, best = min(timed)
     return best, t, len(timed)
+
+
+def autoschedule_strategy(name: str, n: int, trials: int = 64, seed: int = 0, bf16: bool = False,
+                          jobs: int = 8) -> list[tuple[float, tuple[int, ...]]]:
+    """loop-explore of the restatement with one of the reference's PRT
+    strategies ("tile_oo" or "tile_pprprp_vr", src/xtc/search/strategies.py:
+    739-826, restated in xtc_amd/search/strategies.py): `trials` seeded
+    random samples for an n^3 fp32 matmul, each compiled as its own object
+    and timed once (min_repeat_ms 20).  Returns [(seconds per call, tiles)]
+    sorted fastest first; tiles as schedule_lib takes them."""
+    import concurrent.futures as cf
+
+    from xtc_amd.cli.explore import build_graph
+    from xtc_amd.search.strategies import Strategies
+
+    graph = build_graph("matmul", [n, n, n], "float32")
+    strategy = Strategies.create(name, graph, threads=threads())
+    names = strategy.sample_names
+    samples = list(strategy.sample(trials, seed=seed))
+    if name == "tile_oo":
+        # tile_oo's sample is (i1, j1, k1); the restatement takes (i1, k1, j1)
+        tiles = [(x[0], x[2], x[1]) for x in samples]
+    elif name.startswith("tile_pprprp"):
+        tiles = [pprprp_tiles(strategy, x) for x in samples]
+    else:
+        raise ValueError(f"no CPU restatement of strategy {name} (sample names {names})")
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(lambda t: schedule_lib(*t), tiles))
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    if bf16:
+        from xtc_amd.utils.bf16 import round_to_bf16
+
+        a, b = round_to_bf16(a), round_to_bf16(b)
+    return sorted((time_schedule(t, a, b, repeat=1, min_repeat_ms=20), t) for t in tiles)
 
 
 def autoschedule_matmul(a: np.ndarray, b: np.ndarray, repeat: int = 2, min_repeat_ms: int = 50) -> tuple[int, float]:

@@ -234,3 +234,32 @@ def test_cpu_backend_single_schedule_builds_are_exact():
         lib.xtc_cpu_sched_payload.argtypes = [ctypes.c_void_p] * 3
         lib.xtc_cpu_sched_payload(a.ctypes.data, b.ctypes.data, c.ctypes.data)
         np.testing.assert_array_equal(c, want, err_msg=str(tiles))
+
+
+def test_cpu_backend_pprprp_schedules_are_exact_and_follow_the_strategy():
+    # tile_pprprp_vr samples of a 64 x 96 x 48 matmul, each built as its own
+    # object with the sample's 7 tile extents: exact on integer inputs
+    import ctypes
+
+    from oracle import cpu_baseline as cb
+    from xtc_amd.cli.explore import build_graph
+    from xtc_amd.search.strategies import Strategies
+
+    m, n, k = 64, 96, 48
+    strategy = Strategies.create("tile_pprprp_vr", build_graph("matmul", [m, n, k], "float32"), threads=4)
+    samples = list(strategy.sample(6, seed=0))
+    a = R.np_init((m, k), "float32")
+    b = R.np_init((k, n), "float32")
+    want = R.matmul(a, b).astype(np.float32)
+    for x in samples:
+        tiles = cb.pprprp_tiles(strategy, x)
+        i1, i2, i3, j1, j2, j3, k1 = tiles
+        # nested extents of one axis divide each other, as factors_to_sizes gives them
+        assert m % i1 == 0 and i1 % i2 == 0 and i2 % i3 == 0 and n % j1 == 0 and j1 % j2 == 0 and j2 % j3 == 0
+        assert k % k1 == 0 and j3 >= 16  # the vector filter of tile_pprprp_vr
+        lib = cb.schedule_lib(*tiles)
+        lib.xtc_cpu_sched_configure(m, n, k)
+        c = np.full((m, n), np.nan, np.float32)
+        lib.xtc_cpu_sched_payload.argtypes = [ctypes.c_void_p] * 3
+        lib.xtc_cpu_sched_payload(a.ctypes.data, b.ctypes.data, c.ctypes.data)
+        np.testing.assert_array_equal(c, want, err_msg=str(tiles))
