@@ -105,7 +105,10 @@ int xtc_hip_event_destroy(void *event);
 
 /* ------------------------------------------------------ operator entry points */
 
-enum xtc_hip_dtype { XTC_HIP_F32 = 0, XTC_HIP_BF16 = 1 };
+/* Operand types.  fp32 and bf16 operands accumulate and store fp32; fp64
+ * operands accumulate and store fp64 (the float64 graphs that the reference's
+ * MLIR backend lowers, MlirOps.py:194-195,234,339). */
+enum xtc_hip_dtype { XTC_HIP_F32 = 0, XTC_HIP_BF16 = 1, XTC_HIP_F64 = 2 };
 
 /* Kernel template parameters a schedule maps to (block tile BM x BN, K slab
  * BK, WGM x WGN waves).  All zero means "library default for the shape". */
@@ -113,7 +116,8 @@ typedef struct {
   int bm, bn, bk, wgm, wgn;
 } xtc_hip_tile;
 
-/* C[M,N] = relu?( op(A)[M,K] @ op(B)[K,N] + bias[N]? ), fp32 output.
+/* C[M,N] = relu?( op(A)[M,K] @ op(B)[K,N] + bias[N]? ): fp32 output (and fp32
+ * bias) for fp32 / bf16 operands, fp64 output and bias for fp64 operands.
  * Replaces the scheduled linalg.fill + linalg.matmul pair of
  * MlirOperatorMatmul.generate_op (src/xtc/backends/mlir/MlirOps.py:189-270),
  * with XTCOperMatmul semantics (src/xtc/graphs/xtc/operators.py:159-221):
@@ -126,7 +130,7 @@ typedef struct {
  * transposed storage, src/xtc/runtimes/types/ndarray.py:70-102).  With
  * trans_a, A is read from At[K][lda >= M]; with trans_b, B from Bt[N][ldb >= K]. */
 typedef struct {
-  int dtype;             /* xtc_hip_dtype of A and B; C is always fp32 */
+  int dtype;             /* xtc_hip_dtype of A and B; C is fp64 for XTC_HIP_F64, else fp32 */
   int M, N, K;
   int lda, ldb, ldc;     /* row strides in elements of the stored matrices, 0 = dense */
   xtc_hip_tile tile;
@@ -140,10 +144,12 @@ typedef struct {
   int trans_b;           /* 1: B stored transposed, [N][ldb] */
   int stages;            /* pipeline depth (LDS stages), 0 = the kernel's default;
                             xtc_hip_matmul_pipeline_depths lists the legal ones */
+  double relu_threshold_f64; /* the relu threshold of XTC_HIP_F64 calls (an fp32
+                                threshold cannot hold every fp64 value) */
 } xtc_hip_matmul_desc;
 
 int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B,
-                   float *C, const float *bias);
+                   void *C, const void *bias);
 
 /* Per-device scratch of xtc_hip_matmul_noalloc: 64 MiB. */
 #define XTC_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
@@ -163,14 +169,16 @@ int xtc_hip_matmul(const xtc_hip_matmul_desc *desc, const void *A, const void *B
  * calls that overlap on one device race, so callers order them (one stream,
  * or a wait between streams). */
 int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc *desc, const void *A,
-                           const void *B, float *C, const float *bias);
+                           const void *B, void *C, const void *bias);
 
 /* O[b,oh,ow,f] = relu?( sum_{r,s,c} Ipad[b,oh*sh+r,ow*sw+s,c] * W[r,s,c,f] )
  * NHWC x RSCF -> NHWC (XTCOperConv2D, operators.py:252-347;
  * MlirOperatorConv2D, MlirOps.py:304-441).  Ipad is I padded by
  * (pad_top, pad_bottom, pad_left, pad_right) with pad_value: the XTCOperPad2D
  * producer (operators.py:350-591, MlirOps.py:719-735) fused into the loader.
- * C must be a multiple of 4 (fp32) or 8 (bf16). */
+ * Output and bias are fp32 for fp32 / bf16 operands and fp64 for fp64 ones.
+ * Channel counts that are not whole 16-byte vectors are staged with zero
+ * channels (or run on a scalar kernel when the filters are not either). */
 typedef struct {
   int dtype;
   int N, H, W, C;        /* unpadded input */
@@ -185,15 +193,21 @@ typedef struct {
   int relu;
   float relu_threshold;
   void *stream;
+  double relu_threshold_f64; /* XTC_HIP_F64 calls: the relu threshold ... */
+  double pad_value_f64;      /* ... and the pad value, in fp64 */
 } xtc_hip_conv2d_desc;
 
 int xtc_hip_conv2d(const xtc_hip_conv2d_desc *desc, const void *input,
-                   const void *weight, float *out, const float *bias);
+                   const void *weight, void *out, const void *bias);
 
 /* y[i] = max(x[i], threshold) over n fp32 elements (XTCOperRelu forward,
  * operators.py:224-249); x == y allowed. */
 int xtc_hip_relu(const float *x, float *y, uint64_t n, float threshold,
                  void *stream);
+
+/* The same over fp64 elements. */
+int xtc_hip_relu_f64(const double *x, double *y, uint64_t n, double threshold,
+                     void *stream);
 
 /* Constant padding of a row-major fp32 tensor of rank <= 8: out has shape
  * shape[d] + before[d] + after[d]; border = value, interior = input
@@ -201,6 +215,11 @@ int xtc_hip_relu(const float *x, float *y, uint64_t n, float threshold,
 int xtc_hip_pad(const float *x, float *y, int ndim, const int64_t *shape,
                 const int64_t *before, const int64_t *after, float value,
                 void *stream);
+
+/* The same over fp64 elements. */
+int xtc_hip_pad_f64(const double *x, double *y, int ndim, const int64_t *shape,
+                    const int64_t *before, const int64_t *after, double value,
+                    void *stream);
 
 /* Round-to-nearest-even fp32 -> bf16 (stored as uint16) and back. */
 int xtc_hip_cast_f32_to_bf16(const float *x, uint16_t *y, uint64_t n, void *stream);
@@ -284,9 +303,10 @@ void xtc_hip_evaluate(double *results, int repeat, int number, int min_repeat_ms
                       void (*func)(void), void **args, int nargs);
 
 /* Measured peak multiply-accumulates per second of the current device for
- * dtype ("float32", "bfloat16"), the device counterpart of the reference's
+ * dtype ("float32", "bfloat16", "float64"), the device counterpart of the reference's
  * evaluate_flops microbenchmark (evaluate_flops.c:431-494): a register-only
- * loop of independent MFMAs (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16)
+ * loop of independent MFMAs (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16,
+ * v_mfma_f64_16x16x4_f64)
  * on every CU, one wave per SIMD and two workgroups per CU, timed with events
  * over three batches of five ~20 ms launches, best batch.  XTC counts one op
  * per FMA (operation.py:76-82), so this is half the FLOP/s figure.  Operands

@@ -99,7 +99,7 @@ def test_unfused_pad_and_standalone_relu():
     assert [l.kind for l in plan.launches] == ["pad", "relu"]
     pad = plan.launches[0]
     assert pad.attrs["pads"] == [(0, 0), (1, 2), (1, 2), (0, 0)] and pad.attrs["value"] == -1.0
-    assert plan.launches[1].attrs == {"threshold": 0.5, "n": 2 * 8 * 8 * 3}
+    assert plan.launches[1].attrs == {"threshold": 0.5, "n": 2 * 8 * 8 * 3, "dtype": "float32"}
 
 
 def test_bias_add_fuses_before_relu():
@@ -137,7 +137,45 @@ def test_unsupported_operator_and_dtype_raise():
     with pytest.raises(UnsupportedGraph):
         Backend(gb.graph)
     with pytest.raises(UnsupportedGraph):
-        Backend(_matmul(16, 16, 16, "float64"))
+        Backend(_matmul(16, 16, 16, "int32"))
+
+
+def test_float64_graphs_lower_to_fp64_launches(tmp_path):
+    # float64 matmul / conv2d / relu / pad, as the reference's MLIR backend
+    # lowers them (MlirOps.py:194-195,234,339,463,616): fp64 kernels, fp64
+    # outputs, thresholds and pad values passed as C doubles
+    x = O.tensor((8, 14, 14, 16), "float64", name="I")
+    w = O.tensor((3, 3, 16, 32), "float64", name="W")
+    with O.graph(name="conv64") as gb:
+        c = O.conv2d(O.pad2d(x, padding=1, axes=(1, 2), name="pad", constant_value=0.3), w, name="conv")
+        r = O.relu(c, name="relu", threshold=0.1)
+        O.pad(r, padding=(0, 1), name="post")
+    b = Backend(gb.graph)
+    kinds = [(ln.kind, ln.attrs.get("dtype")) for ln in b.plan.launches]
+    assert kinds == [("conv2d", "float64"), ("pad", "float64")]
+    cfgs = b.get_compiler().kernel_configs(b.get_scheduler().schedule())
+    assert cfgs["conv"].dtype == "float64" and cfgs["conv"].tile in legal_tiles("float64", True)
+    src = generate_payload(b.plan, cfgs, "conv64", 0, True)
+    assert "XTC_HIP_F64" in src and "xtc_hip_pad_f64" in src
+    assert ", 0.1, 0.3};" in src  # relu_threshold_f64, pad_value_f64: exact doubles
+    module = b.get_compiler(dump_file=str(tmp_path / "conv64")).compile(b.get_scheduler().schedule())
+    assert Path(module.file_name).exists()
+    # fp64 operands need an fp64 output, as the reference's output dtype is the input's
+    a64 = O.tensor((16, 16), "float64", name="A")
+    b64 = O.tensor((16, 16), "float64", name="B")
+    with O.graph(name="mm64") as gb2:
+        O.matmul(a64, b64, name="C")
+    (ln,) = Backend(gb2.graph).plan.launches
+    assert ln.attrs["dtype"] == "float64"
+    assert legal_tiles("float64", False) and capi.default_tile("float64", False, 4096, 4096, 4096)[0] == (
+        128, 128, 16, 2, 2)
+    # a schedule vectorizing j by 3 does not fit the 2-element fp64 vectors
+    sch = Backend(_matmul(256, 96, 64, "float64")).get_scheduler()
+    sch.tile("j", {"j1": 32, "j2": 3})
+    sch.vectorize(["j2"])
+    with pytest.raises(ScheduleError, match="2-element"):
+        map_gemm(Backend(_matmul(256, 96, 64, "float64")).plan.launches[0].attrs, False,
+                 sch.schedule().node("C"), "strict")
 
 
 def test_operand_layouts_lower_to_transpose_flags(tmp_path):
@@ -152,7 +190,7 @@ def test_operand_layouts_lower_to_transpose_flags(tmp_path):
     assert ln.attrs["trans_a"] and ln.attrs["trans_b"] and (ln.attrs["M"], ln.attrs["N"], ln.attrs["K"]) == (4, 32, 512)
     module = backend.get_compiler(dump_file=str(tmp_path / "ml")).compile(backend.get_scheduler().schedule())
     # the two flags close the descriptor initializer (fields trans_a, trans_b)
-    assert re.search(r"xtc_hip_matmul_desc d = \{.*, 1, 1, 0\};", module.source)
+    assert re.search(r"xtc_hip_matmul_desc d = \{.*, 1, 1, 0, 0.0\};", module.source)
     natural = Backend(_matmul(4, 32, 512)).plan.launches[0].attrs
     assert not natural["trans_a"] and not natural["trans_b"]
 

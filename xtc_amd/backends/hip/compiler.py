@@ -62,7 +62,10 @@ if TYPE_CHECKING:
 
 __all__ = ["HipCompiler", "CompileService", "generate_payload"]
 
-_DTYPE_ENUM = {"float32": "XTC_HIP_F32", "bfloat16": "XTC_HIP_BF16"}
+_DTYPE_ENUM = {"float32": "XTC_HIP_F32", "bfloat16": "XTC_HIP_BF16", "float64": "XTC_HIP_F64"}
+# bytes of the operands and of the output/bias of a GEMM launch per operand dtype
+_IN_BYTES = {"float32": 4, "bfloat16": 2, "float64": 8}
+_OUT_BYTES = {"float32": 4, "bfloat16": 4, "float64": 8}
 _cache_lock = threading.Lock()
 
 
@@ -79,6 +82,15 @@ def _c_float(v: float) -> str:
     if v in (float("inf"), float("-inf")):
         return "(1.0f/0.0f)" if v > 0 else "(-1.0f/0.0f)"
     return f"{float(v)!r}f"
+
+
+def _c_double(v: float) -> str:
+    """`v` as a C double literal: repr round-trips a Python float exactly."""
+    if v != v:
+        return "(0.0/0.0)"
+    if v in (float("inf"), float("-inf")):
+        return "(1.0/0.0)" if v > 0 else "(-1.0/0.0)"
+    return f"{float(v)!r}"
 
 
 def _ptr(plan: Plan, uid: str) -> str:
@@ -175,7 +187,8 @@ def _emit_split_matmul(plan: Plan, ln: Launch, cfg: SplitConfig) -> list[str]:
     (m0, n0) and bias from n0; strides are the whole operands'."""
     a = ln.attrs
     M, N, K = a["M"], a["N"], a["K"]
-    esz = 2 if a["dtype"] == "bfloat16" else 4
+    esz = _IN_BYTES[a["dtype"]]
+    osz = _OUT_BYTES[a["dtype"]]
     ta, tb = bool(a.get("trans_a")), bool(a.get("trans_b"))
     lda, ldb = (M if ta else K), (K if tb else N)
     A, B = _ptr(plan, ln.inputs[0]), _ptr(plan, ln.inputs[1])
@@ -186,16 +199,17 @@ def _emit_split_matmul(plan: Plan, ln: Launch, cfg: SplitConfig) -> list[str]:
         c = p.config
         a_off = p.m0 * esz if ta else p.m0 * lda * esz
         b_off = p.n0 * ldb * esz if tb else p.n0 * esz
-        c_off = (p.m0 * N + p.n0) * 4
+        c_off = (p.m0 * N + p.n0) * osz
         tile = f"{{{c.bm}, {c.bn}, {c.bk}, {c.wgm}, {c.wgn}}}"
         lines.append(
             f"  {{ static const xtc_hip_matmul_desc d = {{{_DTYPE_ENUM[a['dtype']]}, {p.M}, {p.N}, {K}, "
             f"{lda}, {ldb}, {N}, {tile}, {c.split_k}, {c.group_m}, {c.xcd_remap}, {1 if a['relu'] else 0}, "
-            f"{_c_float(a['threshold'])}, 0, {1 if ta else 0}, {1 if tb else 0}, {c.stages}}};"
+            f"{_c_float(a['threshold'])}, 0, {1 if ta else 0}, {1 if tb else 0}, {c.stages}, "
+            f"{_c_double(a['threshold'])}}};"
         )
-        bias_arg = f"(const float *)((const char *){bias} + {p.n0 * 4}ull)" if bias else "0"
+        bias_arg = f"(const void *)((const char *){bias} + {p.n0 * osz}ull)" if bias else "0"
         call = (f"xtc_hip_matmul(&d, (const char *){A} + {a_off}ull, (const char *){B} + {b_off}ull, "
-                f"(float *)((char *){C} + {c_off}ull), {bias_arg})")
+                f"(void *)((char *){C} + {c_off}ull), {bias_arg})")
         where = f'"matmul {ln.node} rows {p.m0}+{p.M} cols {p.n0}+{p.N}"'
         lines.append(f"    if ((rc = {call})) {{ record(rc, {where}); return; }} }}")
     return lines
@@ -218,37 +232,50 @@ def _emit_launch(plan: Plan, ln: Launch, cfg: GemmConfig | SplitConfig | None, i
             f"{1 if a['relu'] else 0}, {_c_float(a['threshold'])}, 0"
         )
         if ln.kind == "matmul":
-            trans = f", {1 if a.get('trans_a') else 0}, {1 if a.get('trans_b') else 0}, {cfg.stages}"
+            trans = (f", {1 if a.get('trans_a') else 0}, {1 if a.get('trans_b') else 0}, {cfg.stages}, "
+                     f"{_c_double(a['threshold'])}")
             lines.append(
                 f"  {{ static const xtc_hip_matmul_desc d = {{{_DTYPE_ENUM[a['dtype']]}, "
                 f"{a['M']}, {a['N']}, {a['K']}, 0, 0, 0, {common}{trans}}};"
             )
-            call = f"xtc_hip_matmul(&d, {_ptr(plan, ln.inputs[0])}, {_ptr(plan, ln.inputs[1])}, (float *){dst}, (const float *){bias})"
+            call = f"xtc_hip_matmul(&d, {_ptr(plan, ln.inputs[0])}, {_ptr(plan, ln.inputs[1])}, (void *){dst}, (const void *){bias})"
         else:
             pt, pb, pl, pr = a["pads"]
             lines.append(
                 f"  {{ static const xtc_hip_conv2d_desc d = {{{_DTYPE_ENUM[a['dtype']]}, "
                 f"{a['NB']}, {a['H']}, {a['W']}, {a['C']}, {a['F']}, {a['R']}, {a['S']}, "
                 f"{a['stride'][0]}, {a['stride'][1]}, {pt}, {pb}, {pl}, {pr}, {_c_float(a['pad_value'])}, "
-                f"{common}}};"
+                f"{common}, {_c_double(a['threshold'])}, {_c_double(a['pad_value'])}}};"
             )
-            call = f"xtc_hip_conv2d(&d, {_ptr(plan, ln.inputs[0])}, {_ptr(plan, ln.inputs[1])}, (float *){dst}, (const float *){bias})"
+            call = f"xtc_hip_conv2d(&d, {_ptr(plan, ln.inputs[0])}, {_ptr(plan, ln.inputs[1])}, (void *){dst}, (const void *){bias})"
         lines.append(f"    if ((rc = {call})) {{ record(rc, {where}); return; }} }}")
     elif ln.kind == "relu":
-        lines.append(
-            f"  if ((rc = xtc_hip_relu((const float *){_ptr(plan, ln.inputs[0])}, (float *){dst}, "
-            f"{a['n']}ull, {_c_float(a['threshold'])}, 0))) {{ record(rc, {where}); return; }}"
-        )
+        if a.get("dtype") == "float64":
+            lines.append(
+                f"  if ((rc = xtc_hip_relu_f64((const double *){_ptr(plan, ln.inputs[0])}, (double *){dst}, "
+                f"{a['n']}ull, {_c_double(a['threshold'])}, 0))) {{ record(rc, {where}); return; }}"
+            )
+        else:
+            lines.append(
+                f"  if ((rc = xtc_hip_relu((const float *){_ptr(plan, ln.inputs[0])}, (float *){dst}, "
+                f"{a['n']}ull, {_c_float(a['threshold'])}, 0))) {{ record(rc, {where}); return; }}"
+            )
     elif ln.kind == "pad":
         nd = len(a["shape"])
         shape = ", ".join(str(d) for d in a["shape"])
         before = ", ".join(str(p[0]) for p in a["pads"])
         after = ", ".join(str(p[1]) for p in a["pads"])
         lines.append(f"  {{ static const int64_t s[{nd}] = {{{shape}}}, b[{nd}] = {{{before}}}, e[{nd}] = {{{after}}};")
-        lines.append(
-            f"    if ((rc = xtc_hip_pad((const float *){_ptr(plan, ln.inputs[0])}, (float *){dst}, {nd}, s, b, e, "
-            f"{_c_float(a['value'])}, 0))) {{ record(rc, {where}); return; }} }}"
-        )
+        if a.get("dtype") == "float64":
+            lines.append(
+                f"    if ((rc = xtc_hip_pad_f64((const double *){_ptr(plan, ln.inputs[0])}, (double *){dst}, {nd}, s, "
+                f"b, e, {_c_double(a['value'])}, 0))) {{ record(rc, {where}); return; }} }}"
+            )
+        else:
+            lines.append(
+                f"    if ((rc = xtc_hip_pad((const float *){_ptr(plan, ln.inputs[0])}, (float *){dst}, {nd}, s, b, e, "
+                f"{_c_float(a['value'])}, 0))) {{ record(rc, {where}); return; }} }}"
+            )
     elif ln.kind == "cast":
         lines.append(
             f"  if ((rc = xtc_hip_cast_f32_to_bf16((const float *){_ptr(plan, ln.inputs[0])}, (uint16_t *){dst}, "

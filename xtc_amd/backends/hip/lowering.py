@@ -31,6 +31,7 @@ __all__ = ["Buffer", "Launch", "Plan", "lower_graph", "UnsupportedGraph"]
 
 F32 = "float32"
 BF16 = "bfloat16"
+F64 = "float64"
 
 
 class UnsupportedGraph(ValueError):
@@ -216,8 +217,9 @@ def lower_graph(graph: Any) -> Plan:
             buffers[n.uid] = Buffer(n.uid, _shape(t_out), _dtype(t_out), "temp")
         if name in ("matmul", "conv2d"):
             in_dt = {_dtype(out_type(u)) for u in n.inputs}
-            if len(in_dt) != 1 or not in_dt <= {F32, BF16}:
-                raise UnsupportedGraph(f"{name} {n.name}: inputs must both be float32 or bfloat16, got {in_dt}")
+            if len(in_dt) != 1 or not in_dt <= {F32, BF16, F64}:
+                raise UnsupportedGraph(
+                    f"{name} {n.name}: inputs must both be float32, float64 or bfloat16, got {in_dt}")
             attrs: dict[str, Any] = {"dtype": in_dt.pop(), "relu": False, "threshold": 0.0, "bias": None}
             fused: list[str] = []
             src_inputs = list(n.inputs)
@@ -273,7 +275,12 @@ def lower_graph(graph: Any) -> Plan:
             if out_uid not in buffers:
                 buffers[out_uid] = Buffer(out_uid, _shape(nodes[out_uid].outputs_types[0]), out_dt, "temp")
             target = out_uid
-            if is_bf16(out_dt):
+            if attrs["dtype"] == F64:
+                # fp64 kernels accumulate and store fp64 (the reference's
+                # output dtype is the input's, operators.py:176-188)
+                if out_dt != F64:
+                    raise UnsupportedGraph(f"{name} {n.name}: float64 inputs need a float64 output, not {out_dt}")
+            elif is_bf16(out_dt):
                 # kernels accumulate and store fp32; a cast kernel narrows it
                 target = out_uid + ".f32"
                 buffers[target] = Buffer(target, buffers[out_uid].shape, F32, "temp")
@@ -285,15 +292,15 @@ def lower_graph(graph: Any) -> Plan:
                 launches.append(Launch("cast", n.name, [target], out_uid, {"n": prod(buffers[out_uid].shape)}))
         elif name == "relu":
             dt = _dtype(t_out)
-            if dt != F32:
-                raise UnsupportedGraph(f"relu {n.name}: only float32 runs standalone")
-            attrs = {"threshold": float(op.attrs.get("threshold", 0)), "n": prod(_shape(t_out))}
+            if dt not in (F32, F64):
+                raise UnsupportedGraph(f"relu {n.name}: only float32 and float64 run standalone")
+            attrs = {"threshold": float(op.attrs.get("threshold", 0)), "n": prod(_shape(t_out)), "dtype": dt}
             launches.append(Launch("relu", n.name, [n.inputs[0]], n.uid, attrs))
             scheduled[n.name] = n
         elif name in ("pad", "pad2d"):
             dt = _dtype(t_out)
-            if dt != F32:
-                raise UnsupportedGraph(f"{name} {n.name}: only float32 runs standalone")
+            if dt not in (F32, F64):
+                raise UnsupportedGraph(f"{name} {n.name}: only float32 and float64 run standalone")
             ishape = _shape(out_type(n.inputs[0]))
             padding = op.attrs.get("padding")
             rank = len(ishape)
@@ -303,7 +310,7 @@ def lower_graph(graph: Any) -> Plan:
                     per[a % rank] = (int(v[0]), int(v[1]))
             else:
                 per = [(int(padding[0]), int(padding[1]))] * rank
-            attrs = {"shape": ishape, "pads": per, "value": float(op.attrs.get("constant_value", 0))}
+            attrs = {"shape": ishape, "pads": per, "value": float(op.attrs.get("constant_value", 0)), "dtype": dt}
             launches.append(Launch("pad", n.name, [n.inputs[0]], n.uid, attrs))
             scheduled[n.name] = n
         elif name == "reshape":

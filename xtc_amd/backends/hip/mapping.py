@@ -28,8 +28,8 @@ where (b,h,w) form GEMM-M, f GEMM-N and (r,s,c) GEMM-K):
     the other loops are recorded: the MFMA loop over a slab and the wave's
     sub-tiles are always fully unrolled, and the block and wave tiles are
     spread over waves and lanes
-  * vectorize(loop) -> the 16-byte loads and stores of every kernel (4 fp32
-    or 8 bf16 elements): the vectorized loop's extent must be a multiple of
+  * vectorize(loop) -> the 16-byte loads and stores of every kernel (4 fp32,
+    2 fp64 or 8 bf16 elements): the vectorized loop's extent must be a multiple of
     that width, or the schedule is rejected
   * pack_at(local), buffer_at, fuse_producer_at -> always on in these
     kernels (LDS staging of both operands, register-resident output tile,
@@ -168,7 +168,7 @@ def default_conv_tile(attrs: dict[str, Any]) -> tuple[tuple[int, int, int, int, 
     from ...runtimes.hip import capi
 
     _, nb, h, w, c, f, r, s, (sh, sw), (pt, pb, pl, pr) = _attrs_key(attrs, True)
-    dt = capi.XTC_HIP_F32 if attrs["dtype"] == "float32" else capi.XTC_HIP_BF16
+    dt = capi.DTYPE_IDS[attrs["dtype"]]
     cd = capi.Conv2dDesc(dtype=dt, N=nb, H=h, W=w, C=c, F=f, R=r, S=s, stride_h=sh, stride_w=sw, pad_top=pt,
                          pad_bottom=pb, pad_left=pl, pad_right=pr)
     return capi.conv2d_default_tile(cd)
@@ -186,7 +186,7 @@ def _attrs_key(attrs: dict[str, Any], conv: bool) -> tuple[Any, ...]:
 def _depths(key: tuple[Any, ...], conv: bool, tile: tuple[int, int, int, int, int], split_k: int) -> tuple[int, ...]:
     from ...runtimes.hip import capi
 
-    dt = capi.XTC_HIP_F32 if key[0] == "float32" else capi.XTC_HIP_BF16
+    dt = capi.DTYPE_IDS[key[0]]
     if conv:
         _, nb, h, w, c, f, r, s, (sh, sw), (pt, pb, pl, pr) = key
         cd = capi.Conv2dDesc(dtype=dt, N=nb, H=h, W=w, C=c, F=f, R=r, S=s, stride_h=sh, stride_w=sw, pad_top=pt,
@@ -223,7 +223,7 @@ def _requested_depth(sched: HipNodeSchedule, k_dims: list[str], split: bool) -> 
 def _check_vectorize(sched: HipNodeSchedule, dtype: str) -> None:
     from .scheduler import basename
 
-    width = 4 if dtype == "float32" else 8
+    width = {"float32": 4, "float64": 2}.get(dtype, 8)
     for qualified in sched.vectorization:
         name = basename(qualified)
         extent = None

@@ -11,7 +11,8 @@ default) searches; --descript takes a descript YAML spec in place of
 --strategy; --op-name picks a named layer's dims (xtc_amd.artifacts);
 --no-execute compiles without evaluating; --save-temps, --explore-dir, --dump
 keep or print the payloads.  Differences: --backends has only `hip`;
---dtype is float32 or bfloat16 (bfloat16 operands, fp32 results);
+--dtype is float32, float64 (the reference's two) or bfloat16 (bfloat16
+operands, fp32 results);
 --repeat defaults to 5; --huge-pages, --bare-ptr, --child, --mlir-prefix and
 --use-tensors are accepted and change nothing here (device buffers, bare
 pointers, no MLIR).  Extensions: --pad, --search default, --vec-size,
@@ -68,7 +69,7 @@ def main(argv: list[str] | None = None) -> int:
     _bool(p, "--huge-pages", True, "accepted for compatibility: GPU buffers come from the device allocator")
     p.add_argument("--test", nargs="+", type=int, default=[], help="evaluate this sample only")
     p.add_argument("--opt-level", type=int, default=4, help="0-3: evaluate the strategy's default schedule; 4: search")
-    p.add_argument("--dtype", default="float32", choices=["float32", "bfloat16"])
+    p.add_argument("--dtype", default="float32", choices=["float32", "float64", "bfloat16"])
     p.add_argument("--trials", type=int, default=100)
     p.add_argument("--threads", type=int, default=1, help="strategy threads (parallel outer axes)")
     p.add_argument("--max-unroll", type=int, default=None,

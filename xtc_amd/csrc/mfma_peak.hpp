@@ -5,7 +5,7 @@
 // 431-494, which times independent FMA chains in registers).
 //
 // Each wave loads its operand fragments once, then issues `iters` rounds of
-// independent MFMAs into 32 (bf16) or 16 (fp32) accumulators: no memory
+// independent MFMAs into 32 (bf16) or 16 (fp32, fp64) accumulators: no memory
 // traffic and no dependency stall inside a round, so the time is the matrix
 // cores' issue rate at the operands' switching activity.  One workgroup of 4
 // waves per SIMD quad (one wave per SIMD), two workgroups per CU.  The
@@ -85,6 +85,42 @@ __global__ void __launch_bounds__(kThreads) mfma_peak_f32(const float* __restric
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += acc[i][j][0] + acc[i][j][3];
   out[blockIdx.x * kThreads + threadIdx.x] = s;
+}
+
+// fp64: a round is 2 k-steps of 4 A x 4 B = 32 MFMAs of 16x16x4 f64
+constexpr int kF64Frags = 16;           // 8-byte operands per lane
+constexpr double kF64FmaPerRound = 32.0 * 16 * 16 * 4;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(kThreads) mfma_peak_f64(const double* __restrict__ in, float* __restrict__ out,
+                                                         int iters) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  double a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = in[(wave * kF64Frags + i) * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) b[i] = in[(wave * kF64Frags + 8 + i) * 64 + lane];
+  f64x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+  for (int t = 0; t < iters; ++t) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(b[4 * q + j], a[4 * q + i], acc[i][j], 0, 0, 0);
+  }
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += acc[i][j][0] + acc[i][j][3];
+  out[blockIdx.x * kThreads + threadIdx.x] = (float)s;
 }
 
 }  // namespace peak

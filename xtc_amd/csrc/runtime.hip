@@ -24,6 +24,7 @@
 #include "gemm_bf16_pingpong.hpp"
 #include "gemm_f32_splitwave.hpp"
 #include "gemm_f32_lds.hpp"
+#include "gemm_f64.hpp"
 #include "conv_direct.hpp"
 #include "mfma_peak.hpp"
 #include "registry.hpp"
@@ -446,6 +447,74 @@ __global__ void conv_naive_kernel(const T* I, const T* Wt, float* O, const float
   }
 }
 
+// fp64 forms of the two fallbacks: fp64 operands, accumulation and output.
+__global__ void gemm_naive_f64_kernel(const double* A, const double* B, double* C, const double* bias, int M, int N,
+                                      int K, int lda, int ldb, int ldc, int relu, double thr) {
+  const uint64_t total = (uint64_t)M * N;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int m = (int)(i / N), n = (int)(i % N);
+    double acc = 0.0;
+    for (int k = 0; k < K; ++k) acc = fma(A[(size_t)m * lda + k], B[(size_t)k * ldb + n], acc);
+    if (bias) acc += bias[n];
+    if (relu && acc < thr) acc = thr;
+    C[(size_t)m * ldc + n] = acc;
+  }
+}
+
+__global__ void conv_naive_f64_kernel(const double* I, const double* Wt, double* O, const double* bias, int NB, int H,
+                                      int W, int C, int F, int R, int S, int sh, int sw, int ph, int pw, int OH,
+                                      int OW, double padv, int relu, double thr) {
+  const uint64_t total = (uint64_t)NB * OH * OW * F;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int f = (int)(i % F);
+    const int m = (int)(i / F);
+    const int ow = m % OW, t = m / OW;
+    const int oh = t % OH, b = t / OH;
+    double acc = 0.0;
+    for (int r = 0; r < R; ++r)
+      for (int s = 0; s < S; ++s) {
+        const int ih = oh * sh + r - ph, iw = ow * sw + s - pw;
+        const bool inb = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        for (int c = 0; c < C; ++c) {
+          const double iv = inb ? I[(((size_t)b * H + ih) * W + iw) * C + c] : padv;
+          acc = fma(iv, Wt[(((size_t)r * S + s) * C + c) * F + f], acc);
+        }
+      }
+    if (bias) acc += bias[f];
+    if (relu && acc < thr) acc = thr;
+    O[(size_t)m * F + f] = acc;
+  }
+}
+
+__global__ void relu_f64_kernel(const double* __restrict__ x, double* __restrict__ y, uint64_t n, double thr) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const double v = x[i];
+    y[i] = v < thr ? thr : v;
+  }
+}
+
+__global__ void pad_f64_kernel(const double* __restrict__ x, double* __restrict__ y, PadDims d, uint64_t total,
+                               double value) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    uint64_t rem = i;
+    int64_t src = 0, src_stride = 1;
+    bool inside = true;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      const int64_t o = (int64_t)(rem % (uint64_t)d.out_shape[k]);
+      rem /= (uint64_t)d.out_shape[k];
+      const int64_t sk = o - d.before[k];
+      inside = inside && sk >= 0 && sk < d.in_shape[k];
+      src += sk * src_stride;
+      src_stride *= d.in_shape[k];
+    }
+    y[i] = inside ? x[src] : value;
+  }
+}
+
 // dst[r][c] = src[r][c] for c < C, 0 for C <= c < Cp, over `rows` rows of C
 // (src) and Cp (dst) elements: the channel padding that gives a conv input
 // (rows = N*H*W pixels) or its RSCF weights (rows = R*S taps, C*F and Cp*F
@@ -537,6 +606,50 @@ const GemmEntry* direct_only_entries(int* n) {
   return v.data();
 }
 
+// fp64 tiles (gemm_f64.hpp): 16-deep slabs, WGM x WGN waves of 16x16 fp64
+// MFMA tiles, for matmul and the implicit-GEMM conv loader alike.
+typedef void (*GemmLaunch64)(const GemmArgs64&, dim3, hipStream_t);
+template <int BM, int BN, int WGM, int WGN, bool CONV>
+void launch_gemm_f64(const GemmArgs64& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_f64_kernel<BM, BN, WGM, WGN, CONV>), grid, dim3(WGM * WGN * 64), 0, s, a);
+}
+struct F64Tile {
+  int conv;
+  xtc_hip_tile tile;
+  GemmLaunch64 launch;
+  int lds_bytes() const { return 2 * (tile.bm * (16 + 2) + 16 * (tile.bn + 8)) * 8; }
+};
+#define XTC_F64_TILES(CONV)                                                      \
+  {CONV, {32, 32, 16, 1, 1}, &launch_gemm_f64<32, 32, 1, 1, CONV>},              \
+      {CONV, {64, 32, 16, 2, 1}, &launch_gemm_f64<64, 32, 2, 1, CONV>},          \
+      {CONV, {32, 64, 16, 1, 2}, &launch_gemm_f64<32, 64, 1, 2, CONV>},          \
+      {CONV, {64, 64, 16, 2, 2}, &launch_gemm_f64<64, 64, 2, 2, CONV>},          \
+      {CONV, {128, 64, 16, 2, 2}, &launch_gemm_f64<128, 64, 2, 2, CONV>},        \
+      {CONV, {64, 128, 16, 2, 2}, &launch_gemm_f64<64, 128, 2, 2, CONV>},        \
+      {CONV, {128, 128, 16, 2, 2}, &launch_gemm_f64<128, 128, 2, 2, CONV>}
+const F64Tile kF64Tiles[] = {XTC_F64_TILES(false), XTC_F64_TILES(true)};
+#undef XTC_F64_TILES
+
+const F64Tile* f64_tile(int conv, const xtc_hip_tile& t) {
+  for (const F64Tile& f : kF64Tiles)
+    if (f.conv == conv && same_tile(f.tile, t)) return &f;
+  return nullptr;
+}
+
+// Registry entries of the fp64 tiles, for listing and lookup (their launch
+// goes through f64_tile: the kernel takes fp64 arguments).
+const GemmEntry* f64_entries(int* n) {
+  static const std::vector<GemmEntry> v = [] {
+    std::vector<GemmEntry> out;
+    for (const F64Tile& f : kF64Tiles)
+      out.push_back(GemmEntry{XTC_HIP_F64, f.conv, f.tile.bm, f.tile.bn, f.tile.bk, f.tile.wgm, f.tile.wgn,
+                              f.lds_bytes(), f.tile.wgm * f.tile.wgn * 64, nullptr, nullptr});
+    return out;
+  }();
+  *n = (int)v.size();
+  return v.data();
+}
+
 const GemmEntry* find_entry(int dtype, int conv, const xtc_hip_tile& t) {
   int n = 0;
   const GemmEntry* e = gemm_registry(&n);
@@ -546,6 +659,10 @@ const GemmEntry* find_entry(int dtype, int conv, const xtc_hip_tile& t) {
       return &e[i];
   }
   const GemmEntry* x = direct_only_entries(&n);
+  for (int i = 0; i < n; ++i)
+    if (x[i].dtype == dtype && x[i].conv == conv && same_tile(xtc_hip_tile{x[i].bm, x[i].bn, x[i].bk, x[i].wgm, x[i].wgn}, t))
+      return &x[i];
+  x = f64_entries(&n);
   for (int i = 0; i < n; ++i)
     if (x[i].dtype == dtype && x[i].conv == conv && same_tile(xtc_hip_tile{x[i].bm, x[i].bn, x[i].bk, x[i].wgm, x[i].wgn}, t))
       return &x[i];
@@ -560,6 +677,26 @@ bool has_entry(int dtype, int conv, int bm, int bn, int bk, int wgm, int wgn) {
 // Default tiles.  Chosen by shape class; tuned on MI355X with loop-explore.
 void default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile* t, int* split_k) {
   *split_k = 1;
+  if (dtype == XTC_HIP_F64) {
+    // fp64: the largest tile that still gives every CU a workgroup, then
+    // split K (ragged splits allowed, at least 4 slabs each) until about
+    // 512 workgroups
+    const xtc_hip_tile cand[] = {
+        {128, 128, 16, 2, 2}, {128, 64, 16, 2, 2}, {64, 64, 16, 2, 2}, {64, 32, 16, 2, 1}, {32, 32, 16, 1, 1}};
+    *t = cand[4];
+    for (const xtc_hip_tile& c : cand) {
+      if (N <= 32 && c.bn > 32) continue;  // N-narrow: no half-empty 64-wide tiles
+      if ((int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) >= 256) {
+        *t = c;
+        break;
+      }
+    }
+    const int64_t tiles = (int64_t)((M + t->bm - 1) / t->bm) * ((N + t->bn - 1) / t->bn);
+    int s = 1;
+    while (s < 16 && tiles * s * 2 <= 512 && K / (2 * s) >= 64) s *= 2;
+    *split_k = s;
+    return;
+  }
   auto pick = [&](int bm, int bn, int bk, int wgm, int wgn) {
     if (has_entry(dtype, conv, bm, bn, bk, wgm, wgn)) {
       *t = xtc_hip_tile{bm, bn, bk, wgm, wgn};
@@ -778,6 +915,29 @@ int launch_gemm_common(GemmArgs& a, const GemmEntry* e, int split_k, int stages,
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits);
   const bool ring = e->launch_ring && (stages == 4 || (stages == 0 && splits > 1));
   (ring ? e->launch_ring : e->launch)(a, grid, s);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+// Split-K set-up and grid of an fp64 launch, as launch_gemm_common for the
+// fp32 / bf16 template (fp64 partial planes).
+int launch_f64_common(GemmArgs64& a, const F64Tile* f, int split_k, int group_m, int xcd_remap, Scratch& x) {
+  a.tiles_m = (a.M + f->tile.bm - 1) / f->tile.bm;
+  a.tiles_n = (a.N + f->tile.bn - 1) / f->tile.bn;
+  a.group_m = group_m > 0 ? group_m : 8;
+  a.xcd_remap = xcd_remap;
+  const int kps = split_depth(a.K, split_k, f->tile.bk);
+  const int splits = (a.K + kps - 1) / kps;
+  a.k_per_split = kps;
+  a.partial = nullptr;
+  a.counters = nullptr;
+  if (splits > 1) {
+    a.partial = (double*)x.partials((size_t)splits * a.M * a.N * sizeof(double));
+    if (!a.partial) return 1;
+    a.counters = x.counters((size_t)a.tiles_m * a.tiles_n);
+    if (!a.counters) return 1;
+  }
+  f->launch(a, dim3((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)splits), x.s);
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -1237,6 +1397,7 @@ __global__ void __launch_bounds__(256) transpose_vec_kernel(const T* __restrict_
 // 64 -> 45 us, 256 -> 61 us.
 constexpr int kTransposeTileF32 = 32;
 constexpr int kTransposeTileBf16 = 128;
+constexpr int kTransposeTileF64 = 32;
 
 // Dense [Cc][R] copy of the R x Cc matrix at src (row stride ld_src) in
 // staging buffer `slot`; null on failure (g_last_error set).
@@ -1246,11 +1407,14 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
   void* dst = x.stage(slot, bytes);
   if (!dst) return nullptr;
   const int vec = 16 / elem_bytes;
-  const int vtile = elem_bytes == 4 ? kTransposeTileF32 : kTransposeTileBf16;
+  const int vtile = elem_bytes == 8 ? kTransposeTileF64 : elem_bytes == 4 ? kTransposeTileF32 : kTransposeTileBf16;
   if (R % vec == 0 && Cc % vec == 0 && ld_src % vec == 0 && aligned16(src) && aligned16(dst) &&
       (R + vtile - 1) / vtile <= 65535) {
     dim3 grid((unsigned)((Cc + vtile - 1) / vtile), (unsigned)((R + vtile - 1) / vtile));
-    if (elem_bytes == 4)
+    if (elem_bytes == 8)
+      hipLaunchKernelGGL((transpose_vec_kernel<uint64_t, kTransposeTileF64>), grid, dim3(256), 0, s,
+                         (const uint64_t*)src, (uint64_t*)dst, R, Cc, ld_src);
+    else if (elem_bytes == 4)
       hipLaunchKernelGGL((transpose_vec_kernel<float, kTransposeTileF32>), grid, dim3(256), 0, s, (const float*)src,
                          (float*)dst, R, Cc, ld_src);
     else
@@ -1267,7 +1431,10 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
     fail("transpose: %d rows exceed the grid limit", R);
     return nullptr;
   }
-  if (elem_bytes == 4)
+  if (elem_bytes == 8)
+    hipLaunchKernelGGL(transpose_kernel<uint64_t>, grid, dim3(256), 0, s, (const uint64_t*)src, (uint64_t*)dst, R,
+                       Cc, ld_src);
+  else if (elem_bytes == 4)
     hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, s, (const float*)src, (float*)dst, R, Cc, ld_src);
   else
     hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)src, (uint16_t*)dst, R,
@@ -1281,7 +1448,7 @@ const void* transposed_copy(int slot, const void* src, int R, int Cc, int ld_src
 
 // The kernel family a matmul runs on, chosen from the shape, tile, split,
 // strides and operand alignment in the order of matmul_impl.
-enum class MatmulPath { LdsDmaBt, Naive, LdsDma, Skinny, SplitWave, F32Lds, Generic };
+enum class MatmulPath { LdsDmaBt, Naive, LdsDma, Skinny, SplitWave, F32Lds, F64, Generic };
 
 const char* path_name(MatmulPath p) {
   switch (p) {
@@ -1296,6 +1463,8 @@ const char* path_name(MatmulPath p) {
       return "split-wave fp32";
     case MatmulPath::F32Lds:
       return "LDS-DMA fp32";
+    case MatmulPath::F64:
+      return "fp64";
     default:
       return "generic";
   }
@@ -1336,6 +1505,9 @@ int path_depths(MatmulPath p, const xtc_hip_tile& t, int ring, int* out, int max
     case MatmulPath::Naive:
       tmp[n++] = 1;
       break;
+    case MatmulPath::F64:
+      tmp[n++] = 2;  // register-staged double buffer
+      break;
     default:
       if (ring == 2) tmp[n++] = 4;
       tmp[n++] = 2;
@@ -1364,7 +1536,7 @@ int check_depth(MatmulPath p, const xtc_hip_tile& t, int ring, int stages) {
 // Strides, tile and split of descriptor d after defaults.  Returns 0, or
 // fails.
 int resolve_matmul(const xtc_hip_matmul_desc& d, int* lda, int* ldb, int* ldc, xtc_hip_tile* t, int* split_k) {
-  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16 && d.dtype != XTC_HIP_F64) return fail("bad dtype %d", d.dtype);
   if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail("bad shape %dx%dx%d", d.M, d.N, d.K);
   if (d.stages < 0) return fail("bad pipeline depth %d", d.stages);
   const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
@@ -1387,11 +1559,17 @@ int resolve_matmul(const xtc_hip_matmul_desc& d, int* lda, int* ldb, int* ldc, x
 // with strides lda/ldb (the B^T-direct case is decided before the copies).
 int natural_path(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda, int ldb, int ldc,
                  const void* A, const void* B, const void* C, const void* bias, MatmulPath* path) {
-  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : d.dtype == XTC_HIP_F64 ? 2 : 8;
   const bool vec_ok = lda % vec == 0 && ldb % vec == 0 && d.K % vec == 0 && d.N % vec == 0 && aligned16(A) &&
                       aligned16(B);
   if (!vec_ok) {
     *path = MatmulPath::Naive;
+    return 0;
+  }
+  if (d.dtype == XTC_HIP_F64) {
+    if (!f64_tile(0, t))
+      return fail("no fp64 matmul kernel instance for tile %dx%dx%d waves %dx%d", t.bm, t.bn, t.bk, t.wgm, t.wgn);
+    *path = MatmulPath::F64;
     return 0;
   }
   if (!find_entry(d.dtype, 0, t))
@@ -1412,8 +1590,32 @@ int natural_path(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_
 
 // xtc_hip_matmul with its scratch taken from `x` (whose stream is the
 // descriptor's).
-int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, float* C, const float* bias,
+// The fp64 GEMM of descriptor d on A/B with strides lda/ldb (after any
+// transposed copy): the fp64 MFMA kernel, split-K partials in fp64.
+int launch_f64_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int lda, int ldb, int ldc,
+                    const void* A, const void* B, void* C, const void* bias, Scratch& x) {
+  const F64Tile* f = f64_tile(0, t);
+  GemmArgs64 a;
+  memset(&a, 0, sizeof(a));
+  a.A = (const double*)A;
+  a.B = (const double*)B;
+  a.C = (double*)C;
+  a.bias = (const double*)bias;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.relu = d.relu;
+  a.relu_threshold = d.relu_threshold_f64;
+  return launch_f64_common(a, f, split_k, d.group_m, d.xcd_remap, x);
+}
+
+int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, void* Cv, const void* biasv,
                 Scratch& x) {
+  float* C = (float*)Cv;
+  const float* bias = (const float*)biasv;
   if (!A || !B || !C) return fail("null operand");
   int lda, ldb, ldc, split_k;
   xtc_hip_tile t;
@@ -1427,7 +1629,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     if (check_depth(MatmulPath::LdsDmaBt, t, 0, d.stages)) return 1;
     return launch_lds_dma_gemm(d, t, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x, true);
   }
-  const int esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
+  const int esz = d.dtype == XTC_HIP_F64 ? 8 : d.dtype == XTC_HIP_F32 ? 4 : 2;
   if (ta) {
     A = transposed_copy(0, A, d.K, d.M, lda, esz, x);
     if (!A) return 1;
@@ -1445,7 +1647,11 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
   if (check_depth(path, t, ring, d.stages)) return 1;
   if (path == MatmulPath::Naive) {
     dim3 grid(grid_for((uint64_t)d.M * d.N, 128));
-    if (d.dtype == XTC_HIP_F32)
+    if (d.dtype == XTC_HIP_F64)
+      hipLaunchKernelGGL(gemm_naive_f64_kernel, grid, dim3(128), 0, s, (const double*)A, (const double*)B,
+                         (double*)Cv, (const double*)biasv, d.M, d.N, d.K, lda, ldb, ldc, d.relu,
+                         d.relu_threshold_f64);
+    else if (d.dtype == XTC_HIP_F32)
       hipLaunchKernelGGL(gemm_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)A,
                          (const float*)B, C, bias, d.M, d.N, d.K, lda, ldb, ldc, d.relu,
                          d.relu_threshold);
@@ -1456,6 +1662,7 @@ int matmul_impl(const xtc_hip_matmul_desc& d, const void* A, const void* B, floa
     HIP_TRY(hipGetLastError());
     return 0;
   }
+  if (path == MatmulPath::F64) return launch_f64_gemm(d, t, split_k, lda, ldb, ldc, A, B, Cv, biasv, x);
   if (path == MatmulPath::LdsDma)
     return launch_lds_dma_gemm(d, t, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x, false);
   if (path == MatmulPath::Skinny) return launch_skinny_gemm(d, split_k, d.stages, lda, ldb, ldc, A, B, C, bias, x);
@@ -1711,18 +1918,23 @@ int xtc_hip_matmul_desc_size(void) { return (int)sizeof(xtc_hip_matmul_desc); }
 int xtc_hip_conv2d_desc_size(void) { return (int)sizeof(xtc_hip_conv2d_desc); }
 
 int xtc_hip_gemm_instance_count(void) {
-  int n = 0, m = 0;
+  int n = 0, m = 0, q = 0;
   gemm_registry(&n);
   direct_only_entries(&m);
-  return n + m;
+  f64_entries(&q);
+  return n + m + q;
 }
 
 int xtc_hip_gemm_instance_get(int index, xtc_hip_gemm_instance* out) {
-  int n = 0, m = 0;
+  int n = 0, m = 0, q = 0;
   const GemmEntry* e = gemm_registry(&n);
   const GemmEntry* x = direct_only_entries(&m);
-  if (index < 0 || index >= n + m || !out) return fail("instance index %d out of range", index);
-  if (index >= n) {
+  const GemmEntry* y = f64_entries(&q);
+  if (index < 0 || index >= n + m + q || !out) return fail("instance index %d out of range", index);
+  if (index >= n + m) {
+    e = y;
+    index -= n + m;
+  } else if (index >= n) {
     e = x;
     index -= n;
   }
@@ -1782,9 +1994,10 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
   if (d.stride_h <= 0 || d.stride_w <= 0 || HP < d.R || WP < d.S) return -fail("bad conv2d descriptor");
   const int OH = (HP - d.R) / d.stride_h + 1;
   const int OW = (WP - d.S) / d.stride_w + 1;
-  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : d.dtype == XTC_HIP_F64 ? 2 : 8;
   const bool padded = d.pad_top || d.pad_bottom || d.pad_left || d.pad_right;
-  if (d.C % vec && d.F % vec == 0 && (!padded || isfinite(d.pad_value))) {
+  const double pad_value = d.dtype == XTC_HIP_F64 ? d.pad_value_f64 : (double)d.pad_value;
+  if (d.C % vec && d.F % vec == 0 && (!padded || isfinite(pad_value))) {
     // xtc_hip_conv2d stages such a conv with zero channels up to the next
     // whole vector and runs the MFMA conv on the copies: describe that kernel
     d.C = (d.C + vec - 1) / vec * vec;
@@ -1805,6 +2018,10 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
     return -fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype, t.bm, t.bn, t.bk,
                  t.wgm, t.wgn);
   const void* p = (const void*)(uintptr_t)256;
+  if (d.dtype == XTC_HIP_F64) {
+    depths[0] = 2;  // the fp64 kernel's register-staged double buffer
+    return 1;
+  }
   // the direct kernel keeps its weight taps in LDS stages or a register
   // ring; the implicit-GEMM loader double-buffers through registers, with
   // three register sets in flight on the tiles that have a ring instance
@@ -1820,16 +2037,16 @@ int xtc_hip_conv2d_pipeline_depths(const xtc_hip_conv2d_desc* desc, int* depths,
   return 1;
 }
 
-int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B, float* C,
-                   const float* bias) {
+int xtc_hip_matmul(const xtc_hip_matmul_desc* desc, const void* A, const void* B, void* C,
+                   const void* bias) {
   if (!desc) return fail("null descriptor");
   if (!current_state()) return fail("xtc_hip_init not called");
   Scratch x{pick_stream(desc->stream)};
   return matmul_impl(*desc, A, B, C, bias, x);
 }
 
-int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc* desc, const void* A, const void* B, float* C,
-                           const float* bias) {
+int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc* desc, const void* A, const void* B, void* C,
+                           const void* bias) {
   if (!desc) return fail("null descriptor");
   DeviceState* dev = current_state();
   if (!dev) return fail("xtc_hip_init not called");
@@ -1841,12 +2058,15 @@ int xtc_hip_matmul_noalloc(const xtc_hip_matmul_desc* desc, const void* A, const
 }
 
 int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const void* weight,
-                   float* out, const float* bias) {
+                   void* outv, const void* biasv) {
   if (!desc) return fail("null descriptor");
   if (!current_state()) return fail("xtc_hip_init not called");
-  if (!input || !weight || !out) return fail("null operand");
+  if (!input || !weight || !outv) return fail("null operand");
+  float* out = (float*)outv;
+  const float* bias = (const float*)biasv;
   const xtc_hip_conv2d_desc& d = *desc;
-  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16) return fail("bad dtype %d", d.dtype);
+  if (d.dtype != XTC_HIP_F32 && d.dtype != XTC_HIP_BF16 && d.dtype != XTC_HIP_F64) return fail("bad dtype %d", d.dtype);
+  const bool f64 = d.dtype == XTC_HIP_F64;
   if (d.N <= 0 || d.H <= 0 || d.W <= 0 || d.C <= 0 || d.F <= 0 || d.R <= 0 || d.S <= 0 ||
       d.stride_h <= 0 || d.stride_w <= 0 || d.pad_top < 0 || d.pad_bottom < 0 ||
       d.pad_left < 0 || d.pad_right < 0)
@@ -1857,26 +2077,32 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   const int OH = (HP - d.R) / d.stride_h + 1;
   const int OW = (WP - d.S) / d.stride_w + 1;
   hipStream_t s = pick_stream(d.stream);
-  const int vec = d.dtype == XTC_HIP_F32 ? 4 : 8;
+  const int vec = d.dtype == XTC_HIP_F32 ? 4 : f64 ? 2 : 8;
   const int M = d.N * OH * OW;
   const int K = d.R * d.S * d.C;
   const bool vec_ok = d.C % vec == 0 && d.F % vec == 0 && aligned16(input) && aligned16(weight);
   const bool padded = d.pad_top || d.pad_bottom || d.pad_left || d.pad_right;
-  if (!vec_ok && d.F % vec == 0 && (!padded || isfinite(d.pad_value))) {
+  if (!vec_ok && d.F % vec == 0 && (!padded || isfinite(f64 ? d.pad_value_f64 : (double)d.pad_value))) {
     // Channels that are not whole 16-byte vectors (C = 3 image inputs): the
     // input and the weights are copied with zero channels up to Cp, a
     // multiple of the vector, and the MFMA conv runs on the copies.  A zero
     // channel adds exact zeros (input 0 or a finite pad value, times a zero
     // weight), so the result is the conv over the C real channels.
     const int Cp = (d.C + vec - 1) / vec * vec;
-    const size_t esz = d.dtype == XTC_HIP_F32 ? 4 : 2;
+    const size_t esz = f64 ? 8 : d.dtype == XTC_HIP_F32 ? 4 : 2;
     const uint64_t pixels = (uint64_t)d.N * d.H * d.W, taps = (uint64_t)d.R * d.S;
     if ((uint64_t)Cp * d.F > 0xffffffffu) return fail("conv2d: %d x %d channels too many to stage", Cp, d.F);
     Scratch x{s};
     void* in_c = x.stage(0, pixels * Cp * esz);
     void* w_c = in_c ? x.stage(1, taps * Cp * d.F * esz) : nullptr;
     if (!in_c || !w_c) return 1;
-    if (d.dtype == XTC_HIP_F32) {
+    if (f64) {  // zero bits are +0.0: the 8-byte copy needs no fp type
+      hipLaunchKernelGGL(pad_channels_kernel<uint64_t>, dim3(grid_for(pixels * Cp, 256)), dim3(256), 0, s,
+                         (const uint64_t*)input, (uint64_t*)in_c, pixels, (uint32_t)d.C, (uint32_t)Cp);
+      hipLaunchKernelGGL(pad_channels_kernel<uint64_t>, dim3(grid_for(taps * Cp * d.F, 256)), dim3(256), 0, s,
+                         (const uint64_t*)weight, (uint64_t*)w_c, taps, (uint32_t)(d.C * d.F),
+                         (uint32_t)(Cp * d.F));
+    } else if (d.dtype == XTC_HIP_F32) {
       hipLaunchKernelGGL(pad_channels_kernel<float>, dim3(grid_for(pixels * Cp, 256)), dim3(256), 0, s,
                          (const float*)input, (float*)in_c, pixels, (uint32_t)d.C, (uint32_t)Cp);
       hipLaunchKernelGGL(pad_channels_kernel<float>, dim3(grid_for(taps * Cp * d.F, 256)), dim3(256), 0, s,
@@ -1891,11 +2117,15 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
     HIP_TRY(hipGetLastError());
     xtc_hip_conv2d_desc dc = d;
     dc.C = Cp;
-    return xtc_hip_conv2d(&dc, in_c, w_c, out, bias);
+    return xtc_hip_conv2d(&dc, in_c, w_c, outv, biasv);
   }
   if (!vec_ok) {
     dim3 grid(grid_for((uint64_t)M * d.F, 128));
-    if (d.dtype == XTC_HIP_F32)
+    if (f64)
+      hipLaunchKernelGGL(conv_naive_f64_kernel, grid, dim3(128), 0, s, (const double*)input, (const double*)weight,
+                         (double*)outv, (const double*)biasv, d.N, d.H, d.W, d.C, d.F, d.R, d.S, d.stride_h,
+                         d.stride_w, d.pad_top, d.pad_left, OH, OW, d.pad_value_f64, d.relu, d.relu_threshold_f64);
+    else if (d.dtype == XTC_HIP_F32)
       hipLaunchKernelGGL(conv_naive_kernel<float>, grid, dim3(128), 0, s, (const float*)input,
                          (const float*)weight, out, bias, d.N, d.H, d.W, d.C, d.F, d.R, d.S,
                          d.stride_h, d.stride_w, d.pad_top, d.pad_left, OH, OW, d.pad_value,
@@ -1919,6 +2149,35 @@ int xtc_hip_conv2d(const xtc_hip_conv2d_desc* desc, const void* input, const voi
   if (!e)
     return fail("no conv2d kernel instance for dtype %d tile %dx%dx%d waves %dx%d", d.dtype,
                 t.bm, t.bn, t.bk, t.wgm, t.wgn);
+  if (f64) {
+    GemmArgs64 a;
+    memset(&a, 0, sizeof(a));
+    a.A = (const double*)input;
+    a.B = (const double*)weight;
+    a.C = (double*)outv;
+    a.bias = (const double*)biasv;
+    a.M = M;
+    a.N = d.F;
+    a.K = K;
+    a.lda = K;
+    a.ldb = d.F;
+    a.ldc = d.F;
+    a.relu = d.relu;
+    a.relu_threshold = d.relu_threshold_f64;
+    a.cH = d.H;
+    a.cW = d.W;
+    a.cC = d.C;
+    a.cOH = OH;
+    a.cOW = OW;
+    a.cS = d.S;
+    a.cSH = d.stride_h;
+    a.cSW = d.stride_w;
+    a.cPH = d.pad_top;
+    a.cPW = d.pad_left;
+    a.pad_value = d.pad_value_f64;
+    Scratch x{s};
+    return launch_f64_common(a, f64_tile(1, t), split_k, d.group_m, d.xcd_remap, x);
+  }
   if (direct_conv_applies(d, t, split_k, OH, OW, input, weight, out, bias))
     return launch_direct_conv(d, t, OH, OW, input, weight, out, bias, s);
   if (!e->launch)
@@ -1992,6 +2251,38 @@ int xtc_hip_pad(const float* x, float* y, int ndim, const int64_t* shape, const 
   }
   hipLaunchKernelGGL(pad_kernel, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
                      x, y, d, total, value);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_relu_f64(const double* x, double* y, uint64_t n, double threshold, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (n == 0) return 0;
+  if (!x || !y) return fail("null operand");
+  hipLaunchKernelGGL(relu_f64_kernel, dim3(grid_for(n, 256)), dim3(256), 0, pick_stream(stream), x, y, n, threshold);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_pad_f64(const double* x, double* y, int ndim, const int64_t* shape, const int64_t* before,
+                    const int64_t* after, double value, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (ndim < 1 || ndim > 8) return fail("pad: rank %d unsupported", ndim);
+  if (!x || !y || !shape || !before || !after) return fail("null operand");
+  PadDims d;
+  memset(&d, 0, sizeof(d));
+  d.ndim = ndim;
+  uint64_t total = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (shape[k] < 0 || before[k] < 0 || after[k] < 0) return fail("pad: negative extent");
+    d.in_shape[k] = shape[k];
+    d.before[k] = before[k];
+    d.out_shape[k] = shape[k] + before[k] + after[k];
+    total *= (uint64_t)d.out_shape[k];
+  }
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(pad_f64_kernel, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream), x, y, d, total,
+                     value);
   HIP_TRY(hipGetLastError());
   return 0;
 }
@@ -2236,18 +2527,20 @@ double xtc_hip_evaluate_flops_operands(const char* dtype, int operands) {
   }
   const bool bf16 = dtype && !strcmp(dtype, "bfloat16");
   const bool f32 = dtype && !strcmp(dtype, "float32");
-  if ((!bf16 && !f32) || operands < 0 || operands > 2) {
+  const bool f64 = dtype && !strcmp(dtype, "float64");
+  if ((!bf16 && !f32 && !f64) || operands < 0 || operands > 2) {
     fail("evaluate_flops: unsupported dtype %s or operands %d", dtype ? dtype : "(null)", operands);
     return 0.0;
   }
   using namespace peak;
   const int blocks = 2 * (d->cus > 0 ? d->cus : 256);
   const size_t waves = (size_t)blocks * (kThreads / 64);
-  const size_t words = waves * 64 * (bf16 ? kBf16Frags * 8 : kF32Frags);  // bf16 halves or floats
+  const size_t words = waves * 64 * (bf16 ? kBf16Frags * 8 : f64 ? kF64Frags : kF32Frags);  // bf16 halves, floats, doubles
   // operand words: the reference's integers 1 + i % 127 (evaluate_flops.c:466-469),
   // zeros, or uniform [-1, 1) from a fixed LCG (bf16: rounded to nearest even)
   std::vector<uint16_t> h16(bf16 ? words : 0);
-  std::vector<float> h32(bf16 ? 0 : words);
+  std::vector<float> h32(bf16 || f64 ? 0 : words);
+  std::vector<double> h64(f64 ? words : 0);
   uint64_t lcg = 0x9e3779b97f4a7c15ull;
   for (size_t i = 0; i < words; ++i) {
     float v = 0.f;
@@ -2261,19 +2554,24 @@ double xtc_hip_evaluate_flops_operands(const char* dtype, int operands) {
       unsigned u;
       memcpy(&u, &v, 4);
       h16[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else if (f64) {
+      h64[i] = v;
     } else {
       h32[i] = v;
     }
   }
-  const size_t in_bytes = words * (bf16 ? 2 : 4);
+  const size_t in_bytes = words * (bf16 ? 2 : f64 ? 8 : 4);
   void *in = nullptr, *out = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   double best = 0.0;
   // ~20 ms per launch at the datasheet rate
   const int iters = bf16 ? 48000 : 12000;
-  const double fmas = (double)waves * iters * (bf16 ? kBf16FmaPerRound : kF32FmaPerRound);
+  const double fmas = (double)waves * iters * (bf16 ? kBf16FmaPerRound : f64 ? kF64FmaPerRound : kF32FmaPerRound);
   auto launch = [&]() {
-    if (bf16)
+    if (f64)
+      hipLaunchKernelGGL(mfma_peak_f64, dim3(blocks), dim3(kThreads), 0, d->stream, (const double*)in, (float*)out,
+                         iters);
+    else if (bf16)
       hipLaunchKernelGGL(mfma_peak_bf16, dim3(blocks), dim3(kThreads), 0, d->stream, (const u32x4*)in,
                          (float*)out, iters);
     else
@@ -2281,7 +2579,7 @@ double xtc_hip_evaluate_flops_operands(const char* dtype, int operands) {
                          (float*)out, iters);
   };
   bool ok = hipMalloc(&in, in_bytes) == hipSuccess && hipMalloc(&out, (size_t)blocks * kThreads * 4) == hipSuccess &&
-            hipMemcpyAsync(in, bf16 ? (const void*)h16.data() : (const void*)h32.data(), in_bytes,
+            hipMemcpyAsync(in, bf16 ? (const void*)h16.data() : f64 ? (const void*)h64.data() : (const void*)h32.data(), in_bytes,
                            hipMemcpyHostToDevice, d->stream) == hipSuccess &&
             hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess;
   if (ok) {

@@ -19,6 +19,7 @@ __all__ = [
     "HipError",
     "XTC_HIP_F32",
     "XTC_HIP_BF16",
+    "XTC_HIP_F64",
     "Tile",
     "MatmulDesc",
     "Conv2dDesc",
@@ -33,6 +34,7 @@ INCLUDE_PATH = Path(__file__).resolve().parents[3] / "include"
 
 XTC_HIP_F32 = 0
 XTC_HIP_BF16 = 1
+XTC_HIP_F64 = 2
 
 
 class HipError(RuntimeError):
@@ -71,6 +73,7 @@ class MatmulDesc(ctypes.Structure):
         ("trans_a", ctypes.c_int),
         ("trans_b", ctypes.c_int),
         ("stages", ctypes.c_int),
+        ("relu_threshold_f64", ctypes.c_double),
     ]
 
 
@@ -98,6 +101,8 @@ class Conv2dDesc(ctypes.Structure):
         ("relu", ctypes.c_int),
         ("relu_threshold", ctypes.c_float),
         ("stream", ctypes.c_void_p),
+        ("relu_threshold_f64", ctypes.c_double),
+        ("pad_value_f64", ctypes.c_double),
     ]
 
 
@@ -153,6 +158,20 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             ctypes.POINTER(ctypes.c_int64),
             ctypes.POINTER(ctypes.c_int64),
             _f,
+            _vp,
+        ],
+    ),
+    "xtc_hip_relu_f64": (_i, [_vp, _vp, _u64, ctypes.c_double, _vp]),
+    "xtc_hip_pad_f64": (
+        _i,
+        [
+            _vp,
+            _vp,
+            _i,
+            ctypes.POINTER(ctypes.c_int64),
+            ctypes.POINTER(ctypes.c_int64),
+            ctypes.POINTER(ctypes.c_int64),
+            ctypes.c_double,
             _vp,
         ],
     ),
@@ -248,7 +267,7 @@ def gemm_instances() -> list[dict[str, Any]]:
         check(L.xtc_hip_gemm_instance_get(i, ctypes.byref(inst)), "gemm_instance_get")
         out.append(
             {
-                "dtype": "float32" if inst.dtype == XTC_HIP_F32 else "bfloat16",
+                "dtype": DTYPE_NAMES[inst.dtype],
                 "conv": bool(inst.conv),
                 "tile": inst.tile.as_tuple(),
                 "lds_bytes": inst.lds_bytes,
@@ -258,7 +277,9 @@ def gemm_instances() -> list[dict[str, Any]]:
     return out
 
 
-_DTYPE_IDS = {"float32": XTC_HIP_F32, "bfloat16": XTC_HIP_BF16}
+_DTYPE_IDS = {"float32": XTC_HIP_F32, "bfloat16": XTC_HIP_BF16, "float64": XTC_HIP_F64}
+DTYPE_IDS = _DTYPE_IDS
+DTYPE_NAMES = {v: k for k, v in _DTYPE_IDS.items()}
 
 
 def default_tile(dtype: str, conv: bool, M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int], int]:
