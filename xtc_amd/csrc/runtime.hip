@@ -561,17 +561,25 @@ template <int TH, int TW, int WM, int WN, int HALO_BYTES, int WRING>
 void launch_conv_direct(const DirectConvArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((conv_direct_f32<TH, TW, WM, WN, HALO_BYTES, WRING>), grid, dim3(dconv::NT), 0, s, a);
 }
+template <int TH, int TW, int WRING>
+void launch_conv_direct_3x3s1(const DirectConvArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((conv_direct_f32_3x3s1<TH, TW, WRING>), grid, dim3(dconv::NT), 0, s, a);
+}
 struct DirectConvTile {
   xtc_hip_tile tile;
   int th, tw, halo_bytes;
   int wring;  // 0: weights through dconv::STAGES LDS stages, else register ring depth
   DirectConvLaunch launch;
+  // the same blocks and ring for a 3x3 window at stride 1, its offsets fixed
+  // at compile time (bit-identical to `launch`); null where there is none
+  DirectConvLaunch launch_3x3s1;
   int lds_bytes() const { return halo_bytes + (wring ? 0 : dconv::STAGES * dconv::W_STAGE); }
   int depth() const { return wring ? wring : dconv::STAGES; }
 };
 const DirectConvTile kDirectConv[] = {
-    {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, 0, &launch_conv_direct<8, 8, 2, 2, 32 * 1024, 0>},
-    {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, 3, &launch_conv_direct<8, 14, 1, 4, 48 * 1024, 3>},
+    {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, 0, &launch_conv_direct<8, 8, 2, 2, 32 * 1024, 0>, nullptr},
+    {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, 3, &launch_conv_direct<8, 14, 1, 4, 48 * 1024, 3>,
+     &launch_conv_direct_3x3s1<8, 14, 3>},
 };
 
 bool same_tile(const xtc_hip_tile& a, const xtc_hip_tile& b) {
@@ -1233,7 +1241,8 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int 
   a.tiles_w = (OW + dt->tw - 1) / dt->tw;
   const uint64_t blocks = (uint64_t)d.N * a.tiles_h * a.tiles_w * (d.F / dconv::FB);
   if (blocks > 0x7fffffffu) return fail("conv2d grid too large");
-  dt->launch(a, dim3((unsigned)blocks), s);
+  const bool fixed = dt->launch_3x3s1 && d.R == 3 && d.S == 3 && d.stride_h == 1 && d.stride_w == 1;
+  (fixed ? dt->launch_3x3s1 : dt->launch)(a, dim3((unsigned)blocks), s);
   HIP_TRY(hipGetLastError());
   return 0;
 }
