@@ -1008,6 +1008,27 @@ def test_direct_conv_8x14_ragged(shape):
     np.testing.assert_array_equal(got, ref.conv2d(xpi, wi).astype(np.float32))
 
 
+@pytest.mark.parametrize("r,s", [(3, 3), (3, 2), (2, 3)])
+def test_direct_conv_8x14_bias_relu(r, s):
+    # 3x3 at stride 1 runs the compile-time-offset kernel, the other windows
+    # the general one, on the same tile: bias and relu in the epilogue, two
+    # filter blocks, blocks that overhang the image in H and W
+    x = rng_uniform(51, (2, 19, 33, 64), 0.0, 1.0)
+    w = rng_uniform(52, (r, s, 64, 128), -0.1, 0.1)
+    bias = rng_uniform(53, (128,), -0.3, 0.3)
+    pads = (r // 2, r // 2, s // 2, s // 2)
+    got = run_conv(x, w, pads=pads, tile=(112, 64, 16, 1, 4), relu=True, bias=bias)
+    xp = ref.pad(x, [(0, 0), pads[:2], pads[2:], (0, 0)])
+    want = ref.relu(ref.conv2d(xp, w) + bias)
+    assert ref.scaled_error(got, want, r * s * 64, 1.0, 0.1) <= TOL_F32
+    xi = ref.np_init(x.shape, "float32") % 5
+    wi = ref.np_init(w.shape, "float32") % 3 - 1
+    bi = np.arange(128, dtype=np.float32) % 7 - 3
+    got = run_conv(xi, wi, pads=pads, tile=(112, 64, 16, 1, 4), relu=True, bias=bi)
+    xpi = ref.pad(xi, [(0, 0), pads[:2], pads[2:], (0, 0)])
+    np.testing.assert_array_equal(got, ref.relu(ref.conv2d(xpi, wi) + bi).astype(np.float32))
+
+
 def test_direct_only_conv_tile_rejects_other_shapes():
     x, w = rng_uniform(1, (1, 20, 20, 64)), rng_uniform(2, (3, 3, 64, 64))
     with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
