@@ -459,6 +459,28 @@ def main(argv: list[str] | None = None) -> int:
         tol = 1e-2 if cfg.startswith("C3") else 1e-4
         if not spot_err <= tol:
             raise SystemExit(f"parity spot check failed: scaled error {spot_err} > {tol}")
+    elif cfg == "C4":
+        # first image, first 8 output rows: relu(conv3x3(pad1(x)))
+        x, w = host_in[0][0].astype(np.float64), host_in[1].astype(np.float64)
+        xp = np.pad(x, ((1, 1), (1, 1), (0, 0)))
+        ref = np.zeros((8, 56, 64))
+        for r in range(3):
+            for s in range(3):
+                ref += np.einsum("hwc,cf->hwf", xp[r:r + 8, s:s + 56], w[r, s])
+        ref = np.maximum(ref, 0.0)
+        out = d_out[0].numpy()[0, :8]
+        spot_err = float(np.abs(out - ref).max() / (np.sqrt(576) * np.abs(xp).max() * np.abs(w).max()))
+        if not spot_err <= 1e-4:
+            raise SystemExit(f"parity spot check failed: scaled error {spot_err} > 1e-4")
+    elif cfg == "C5":
+        # first 8 rows: relu(X W1) W2, the error scaled on the second GEMM
+        x, w1, w2 = (a.astype(np.float64) for a in host_in[:3])
+        h = np.maximum(x[:8] @ w1, 0.0)
+        ref = h @ w2
+        out = d_out[0].numpy()[:8]
+        spot_err = float(np.abs(out - ref).max() / (np.sqrt(w2.shape[0]) * np.abs(h).max() * np.abs(w2).max()))
+        if not spot_err <= 1e-4:
+            raise SystemExit(f"parity spot check failed: scaled error {spot_err} > 1e-4")
 
     print(f"[bench] {cfg}: {args.warmup} warmup (at least {args.warmup_ms:g} ms) + {args.steps} timed steps",
           file=sys.stderr, flush=True)
