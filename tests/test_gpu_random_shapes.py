@@ -118,3 +118,51 @@ def test_random_conv_exact(case):
           f"split={split}", flush=True)
     got = run_conv(x, wt, dtype, stride=(sh, sw), pads=pads, pad_value=2.0, tile=tile, split_k=split)
     np.testing.assert_array_equal(got, want)
+
+
+def _direct_conv_cases(n: int, seed: int) -> list[tuple]:
+    """fp32 convs the direct kernel takes (C and F multiples of 64, the block's
+    halo within its LDS buffer): half of them 3x3 at stride 1, which run the
+    compile-time-offset kernel on the 8x14 tile."""
+    rng = np.random.default_rng(seed)
+    out = []
+    halo_pix = {(112, 64, 16, 1, 4): (8, 14, 49152 // 272), (64, 64, 16, 2, 2): (8, 8, 32768 // 272)}
+    while len(out) < n:
+        i = len(out)
+        tile = (112, 64, 16, 1, 4) if i % 3 else (64, 64, 16, 2, 2)
+        th, tw, cap = halo_pix[tile]
+        if i % 2 == 0:
+            r = s = 3
+            sh = sw = 1
+        else:
+            r, s = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+            sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        if ((th - 1) * sh + r) * ((tw - 1) * sw + s) > cap:
+            continue
+        nb = int(rng.integers(1, 4))
+        h, w = int(rng.integers(5, 41)), int(rng.integers(5, 41))
+        c = int(rng.choice([64, 128, 192]))
+        f = int(rng.choice([64, 128]))
+        pads = tuple(int(p) for p in rng.integers(0, 3, size=4))
+        if h + pads[0] + pads[1] < r or w + pads[2] + pads[3] < s:
+            continue
+        out.append((i, nb, h, w, c, f, r, s, sh, sw, pads, tile, bool(rng.integers(2))))
+    return out
+
+
+DIRECT = _direct_conv_cases(24, 2026)
+
+
+@pytest.mark.parametrize("case", DIRECT, ids=[f"dconv{c[0]}-{c[6]}x{c[7]}s{c[8]}{c[9]}" for c in DIRECT])
+def test_random_direct_conv_exact(case):
+    i, nb, h, w, c, f, r, s, sh, sw, pads, tile, with_bias = case
+    rng = np.random.default_rng(3000 + i)
+    x = rng.integers(1, 10, (nb, h, w, c)).astype(np.float32)
+    wt = rng.integers(-4, 5, (r, s, c, f)).astype(np.float32)
+    bias = rng.integers(-3, 4, (f,)).astype(np.float32) if with_bias else None
+    xp = ref.pad(x, [(0, 0), (pads[0], pads[1]), (pads[2], pads[3]), (0, 0)], 2.0)
+    want = ref.relu(ref.conv2d(xp, wt, (sh, sw)) + (bias if with_bias else 0.0)).astype(np.float32)
+    print(f"[random] dconv{i} x={x.shape} w={wt.shape} stride=({sh},{sw}) pads={pads} tile={tile} bias={with_bias}",
+          flush=True)
+    got = run_conv(x, wt, "float32", stride=(sh, sw), pads=pads, pad_value=2.0, tile=tile, relu=True, bias=bias)
+    np.testing.assert_array_equal(got, want)
