@@ -96,6 +96,33 @@ def _vendor_matmul(host_in: list[np.ndarray], dtype: str, steps: int, warmup: in
             "tflops": round(2 * m * n * k / ms / 1e9, 1)}
 
 
+def _vendor_conv(host_in: list[np.ndarray], steps: int, warmup: int, warmup_ms: float) -> dict:
+    """Times torch's conv2d (MIOpen on this image) on the C4 inputs, NHWC
+    (channels_last) fp32 with a 1-pixel zero pad and relu, as a reference
+    point for the vendor library after the same warm-up as the bench's own
+    steps.  MIOpen picks its own algorithm (its numerics are not checked
+    here)."""
+    import torch
+
+    x = torch.from_numpy(host_in[0]).to("cuda:0").permute(0, 3, 1, 2).contiguous(memory_format=torch.channels_last)
+    w = torch.from_numpy(host_in[1]).to("cuda:0").permute(3, 2, 0, 1).contiguous(memory_format=torch.channels_last)
+
+    def step() -> None:
+        torch.relu_(torch.nn.functional.conv2d(x, w, padding=1))
+
+    _warm(step, torch.cuda.synchronize, warmup, warmup_ms)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flop = workloads.flops("C4")
+    return {"library": "torch.nn.functional.conv2d + relu_ (MIOpen), channels_last fp32", "kernel_ms": round(ms, 4),
+            "tflops": round(flop / ms / 1e9, 1)}
+
+
 def _cpu_baseline(cfg: str) -> dict:
     """Times the CPU restatement of XTC's llvmir backend (oracle/) on this
     host, auto-scheduled as loop-explore would: 64 seeded samples each of the
@@ -391,7 +418,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--peak", action="store_true",
                     help="only print the measured MFMA peaks (fp32, bf16; zero, random and the reference's operands)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
-                    help="also time torch.matmul on the same inputs (matmul configs) and report it in config")
+                    help="also time the vendor library on the same inputs and report it in config: torch.matmul "
+                         "(hipBLASLt) for the matmul configs, torch's conv2d (MIOpen) for C4")
     ap.add_argument("--named-ops", action="store_true",
                     help="time every named operation of loop-explore --op-name with its default schedule")
     ap.add_argument("--named-dtype", default="float32", choices=["float32", "bfloat16"],
@@ -556,6 +584,8 @@ def main(argv: list[str] | None = None) -> int:
         }
     if args.vs_hipblaslt and cfg in ("C1", "C2", "C3a", "C3b"):
         line["config"]["vendor"] = _vendor_matmul(host_in, dtype, args.steps, args.warmup, args.warmup_ms)
+    if args.vs_hipblaslt and cfg == "C4":
+        line["config"]["vendor"] = _vendor_conv(host_in, args.steps, args.warmup, args.warmup_ms)
     if not args.no_cpu:
         print(f"[bench] {cfg}: cpu baseline", file=sys.stderr, flush=True)
         try:
