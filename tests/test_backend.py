@@ -629,7 +629,8 @@ def test_conv_pipeline_depths_describe_the_channel_staged_kernel():
 
 
 def _integration_structs():
-    """The ctypes structs of the binding INTEGRATION.md tells maintainers to write."""
+    """The ctypes structs of the binding that the integration guide at the
+    repository root tells maintainers to write (its ctypes snippet)."""
     text = (ROOT / "INTEGRATION.md").read_text()
     block = re.search(r"```python\n(import ctypes\n\nclass Tile.*?)\nlib = ctypes\.CDLL", text, re.S)
     assert block, "INTEGRATION.md: ctypes binding snippet not found"
