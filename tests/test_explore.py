@@ -30,6 +30,29 @@ def test_cli_graphs_follow_the_reference_shapes():
     assert build_graph("relu", [1024], "float32").ops_count() == 1024
 
 
+def test_bf16_graphs_count_and_peak_in_their_operand_dtype(monkeypatch):
+    # a bf16 matmul or conv that stores fp32 computes in bf16: its ops dtype,
+    # hence the peak the explorer divides by, is bfloat16, and a pad2d in
+    # front of a bf16 conv is counted together with the conv, as the
+    # reference counts every node of the first node's dtype (graph.py:190-205)
+    g = build_graph("matmul", [16, 8192, 8192], "bfloat16")
+    assert g.ops_dtype() == "bfloat16" and g.ops_count() == 16 * 8192 * 8192
+    g = build_graph("conv2d", [1, 8, 8, 64, 3, 3, 64, 1, 1], "bfloat16", pad=1)
+    assert g.ops_dtype() == "bfloat16" and g.ops_count() == 8 * 8 * 64 * 9 * 64 + 10 * 10 * 64
+    seen = []
+
+    class _Dev:
+        def evaluate_flops(self, dtype):
+            seen.append(dtype)
+            return 1e15
+
+    import xtc_amd.runtimes.hip.device as device
+
+    monkeypatch.setattr(device, "HipDevice", _Dev)
+    ex = Exploration(build_graph("matmul", [8192, 8192, 8192], "bfloat16"), ExplorationConfig())
+    assert ex.peak_time() == pytest.approx(8192**3 / 1e15) and seen == ["bfloat16"]
+
+
 def _stub(monkeypatch, calls):
     def evaluate_one(self, module):
         calls.append(module.configs)

@@ -79,6 +79,14 @@ class XTCOperation(Operation):
 
     @property
     def ops_dtype(self) -> str:
+        """dtype of the operation's arithmetic.  The reference takes the
+        first output's (src/xtc/graphs/xtc/operation.py:86-89), where inputs
+        and outputs share it.  Under the out_dtype extension (bfloat16
+        operands, float32 result) the arithmetic is the operands', so the
+        first input's dtype is taken when there is one: the same value for
+        every graph the reference builds."""
+        if self._inputs_types:
+            return self._inputs_types[0].constant_dtype
         return self._outputs_types[0].constant_dtype
 
     @property

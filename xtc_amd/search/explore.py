@@ -490,6 +490,9 @@ class Exploration:
         return per["gpu.time"], per
 
     def peak_time(self) -> float:
+        """The graph's time at the device's MFMA peak for the graph's ops
+        dtype (explore.py:619-625): bfloat16 for a bf16 matmul or conv even
+        when it stores float32."""
         peak = self.config.peak_flops
         if peak is None and self.config.backend == "hip":
             from ..runtimes.hip.device import HipDevice
