@@ -266,6 +266,22 @@ def test_iterative_search_records_every_batch(tmp_path, monkeypatch):
     assert 1 <= len(rows) <= 7  # repeated proposals are written once
 
 
+def test_iterative_tile_hip_search_starts_from_the_library_default(tmp_path, monkeypatch):
+    # tile_hip puts the library's own schedule in the first batch, so the
+    # search never ends below it; the reference's strategies do not
+    _stub(monkeypatch, [])
+    g = build_graph("matmul", [1024, 1024, 1024], "float32")
+    cfg = ExplorationConfig(search="iterative", strategy="tile_hip", trials=5, batch=3, seed=2, peak_flops=1e12,
+                            output=str(tmp_path / "h.csv"), jobs=1)
+    ex = Exploration(g, cfg)
+    res = ex.run()
+    assert len(res) == 5 and res[0][0] == list(ex.strategy.default_schedule(2))
+    ex2 = Exploration(g, ExplorationConfig(search="iterative", strategy="tile_oo", trials=3, batch=3, seed=2,
+                                           peak_flops=1e12, output=str(tmp_path / "o.csv"), jobs=1))
+    assert not getattr(ex2.strategy, "starts_from_default", False)
+    assert len(ex2.run()) == 3
+
+
 def _grid_sampler(n, seed):
     import numpy as np
 

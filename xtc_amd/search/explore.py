@@ -648,9 +648,15 @@ class Exploration:
             lambda n, seed: self.strategy.sample(n, seed=seed), c.batch, c.seed, c.optimizer_config
         )
         results: list[tuple[list[int], list[float], int, str]] = []
+        # a strategy that can name the library's own choice for the graph
+        # (tile_hip) puts it in the first batch in place of the optimizer's
+        # last pick: the optimizer then learns from it, and the search never
+        # ends below the default; the optimizer's draws are unchanged
+        start = [list(self.strategy.default_schedule(2))] if getattr(self.strategy, "starts_from_default", False) else []
         for step in range(0, c.trials, c.batch):
             size = min(c.batch, c.trials - step)
-            batch = [list(x) for x in opt.suggest()[:size]]
+            first = start if step == 0 else []
+            batch = first + [list(x) for x in opt.suggest()[: size - len(first)]]
             got = self._run_batch(pool, batch, csv_cb, db_cb, step, c.trials)
             results.extend(got)
             opt.observe(batch, [peak_time / min(t) if code == 0 and t and min(t) > 0 else 0.0 for _, t, code, _ in got])

@@ -574,7 +574,12 @@ class Strategy_HIP(BaseStrategy):
       * stages: unroll of the slab loop (k, or k1 under split-K; c or c1 for conv)
         by the pipeline depth, one of the depths the tile's kernel is
         compiled for on this shape (the default first).
+
+    Its default sample is the library's own choice for the shape, and the
+    iterative search evaluates it in its first batch (starts_from_default).
     """
+
+    starts_from_default = True
 
     def __init__(self, graph: Any, **kwargs: Any) -> None:
         super().__init__(graph, ["bm", "wm", "bn", "wn", "bk", "split_k", "stages"], **kwargs)
