@@ -8,6 +8,7 @@ from __future__ import annotations
 import csv
 import json
 
+import numpy as np
 import pytest
 
 from xtc_amd.backends.hip import Backend
@@ -487,3 +488,32 @@ def test_exploration_config_from_args():
     assert (c.operator, c.trials, c.search, c.seed) == ("conv2d", 7, "exhaustive", 3)
     with pytest.raises(TypeError, match="unknown exploration configuration option"):
         ExplorationConfig.from_args(None, trialz=1)
+
+
+def test_random_inputs_give_seeded_uniform_parameters(tmp_path, monkeypatch):
+    from xtc_amd.search.explore import random_parameters
+    from xtc_amd.utils.bf16 import round_to_bf16
+
+    g = build_graph("matmul", [64, 32, 48], "bfloat16")
+    (a, b), (c,) = random_parameters(g, 7)
+    assert a.shape == (64, 48) and b.shape == (48, 32) and c.shape == (64, 32)
+    assert a.dtype == np.float32 and c.dtype == np.float32
+    assert np.array_equal(a, round_to_bf16(a)) and -1.0 <= a.min() and a.max() <= 1.0
+    a2, _ = random_parameters(g, 7)[0]
+    assert np.array_equal(a, a2) and not np.array_equal(a, random_parameters(g, 8)[0][0])
+    # the CLI hands them to every evaluation and records the seed in the manifest
+    seen = []
+
+    def evaluate_one(self, module):
+        seen.append(self.config.eval_parameters)
+        return [1e-3], 0, ""
+
+    monkeypatch.setattr(Exploration, "evaluate_one", evaluate_one)
+    from xtc_amd.cli.explore import main
+
+    out = tmp_path / "r.csv"
+    assert main(["--operator", "matmul", "--dims", "64", "32", "48", "--dtype", "bfloat16", "--trials", "2",
+                 "--random-inputs", "7", "--peak-flops", "1e12", "--output", str(out), "--jobs", "1", "--quiet"]) == 0
+    assert len(seen) == 2 and all(np.array_equal(p[0][0], a) for p in seen)
+    meta = json.loads(open(f"{out}.meta.json").read())
+    assert meta["args"]["random_inputs"] == 7

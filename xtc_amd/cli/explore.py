@@ -77,6 +77,10 @@ def main(argv: list[str] | None = None) -> int:
                    "so the CPU bound of 256 would only exclude GPU-sized tiles)")
     p.add_argument("--vec-size", type=int, default=16)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--random-inputs", type=int, default=None, metavar="SEED",
+                   help="time (and validate) every sample on seeded uniform[-1,1) inputs, rounded to bfloat16 for "
+                        "bfloat16 tensors, instead of the reference's np_init integers: on MI355X a bf16 GEMM's "
+                        "clock depends on the power its operands draw")
     p.add_argument("--output", default="results.csv")
     p.add_argument("--db-file", help="output json db, for instance: xtc-graphs-db.json")
     _bool(p, "--resume", False, "skip samples already in --output")
@@ -159,6 +163,10 @@ def main(argv: list[str] | None = None) -> int:
     config = ExplorationConfig.from_args(args)
     if args.graph_file:
         config.operator = None
+    if args.random_inputs is not None:
+        from ..search.explore import config_graph, random_parameters
+
+        config.eval_parameters = random_parameters(config_graph(config), args.random_inputs)
     results = Exploration(config).run()
     if not args.quiet and not args.execute:
         ok = sum(1 for _, code, _, _ in results if code == 0)

@@ -47,10 +47,12 @@ from importlib import import_module
 from pathlib import Path
 from typing import Any, Callable
 
+import numpy as np
+
 from .strategies import Strategies
 
 __all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x", "OPERATORS",
-           "build_graph", "operation_dims", "config_graph"]
+           "build_graph", "operation_dims", "config_graph", "random_parameters"]
 
 logger = logging.getLogger("xtc_amd.search")
 
@@ -119,6 +121,7 @@ class ExplorationConfig:
     progress_cls: str = "tqdm"
     debug_compile: bool = False  # log the payload compile commands
     eval_parameters: Any = None  # (inputs, outputs) numpy arrays for every evaluation
+    random_inputs: int | None = None  # the seed of the CLI's eval_parameters (random_parameters), for the manifest
     # filled by Exploration(config).run(): (sample, code, time, backend) per sample
     results: list[Any] = field(default_factory=list)
 
@@ -193,6 +196,26 @@ def build_graph(operator: str, dims: list[int], dtype: str, pad: int = 0, name: 
             O.relu(x, threshold=0, name="O")
         return gb.graph
     raise ValueError(f"unknown operator {operator}")
+
+
+def random_parameters(graph: Any, seed: int) -> tuple[list[np.ndarray], list[np.ndarray]]:
+    """(inputs, outputs) for every evaluation of an exploration: seeded
+    uniform[-1, 1) inputs in graph-input order, rounded to bfloat16 for
+    bfloat16 tensors, and output buffers.  An extension: the reference
+    evaluates on np_init integers (src/xtc/utils/numpy.py:12-19).  On MI355X
+    the power a bf16 GEMM draws, hence its clock, depends on its operands, so
+    a search meant for random data has to time it on random data."""
+    from ..utils.bf16 import host_dtype, round_to_bf16
+
+    rng = np.random.default_rng(seed)
+    ins = []
+    for t in graph.inputs_types:
+        x = rng.uniform(-1.0, 1.0, tuple(t.constant_shape))
+        if str(t.constant_dtype) == "bfloat16":
+            x = round_to_bf16(x.astype(np.float32))
+        ins.append(np.ascontiguousarray(x.astype(host_dtype(t.constant_dtype))))
+    outs = [np.empty(tuple(t.constant_shape), dtype=host_dtype(t.constant_dtype)) for t in graph.outputs_types]
+    return ins, outs
 
 
 def config_graph(config: ExplorationConfig) -> Any:
