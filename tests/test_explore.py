@@ -517,3 +517,49 @@ def test_random_inputs_give_seeded_uniform_parameters(tmp_path, monkeypatch):
     assert len(seen) == 2 and all(np.array_equal(p[0][0], a) for p in seen)
     meta = json.loads(open(f"{out}.meta.json").read())
     assert meta["args"]["random_inputs"] == 7
+
+
+def test_random_inputs_validate_to_a_scaled_bound():
+    """On random inputs the payload's fp32 sums and numpy's differ in the last
+    bits, so np.allclose's atol 1e-8 fails near-zero outputs: the explorer
+    validates those samples to max |diff| <= 1e-4 max |ref| (1e-10 for
+    float64), which still catches a dropped term."""
+    from xtc_amd.search.explore import ExplorationConfig, random_inputs_tolerance
+    from xtc_amd.targets.hip.evaluator import outputs_mismatch
+
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (128, 512)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 128)).astype(np.float32)
+    ref = np.dot(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+    # fp32 sums in another order: k walked backwards, one term at a time
+    got = np.zeros_like(ref)
+    for k in range(511, -1, -1):
+        got += np.outer(a[:, k], b[k, :])
+    assert outputs_mismatch(ref, got, 1e-5, 1e-8) is not None  # np.allclose rejects the rounding
+    assert outputs_mismatch(ref, got, 1e-5, 1e-8, 1e-4) is None
+    dropped = got - np.outer(a[:, 17], b[17, :])  # one k missing
+    assert "max |diff| / max |ref|" in outputs_mismatch(ref, dropped, 1e-5, 1e-8, 1e-4)
+    nan_ref, nan_got = ref.copy(), got.copy()
+    nan_ref[3, 4] = np.nan
+    assert "NaN" in outputs_mismatch(nan_ref, got, 1e-5, 1e-8, 1e-4)
+    nan_got[3, 4] = np.nan
+    assert outputs_mismatch(nan_ref, nan_got, 1e-5, 1e-8, 1e-4) is None
+    assert outputs_mismatch(ref, ref.copy(), 1e-5, 1e-8) is None
+
+    assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "bfloat16")) == 1e-4
+    assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "float32")) == 1e-4
+    assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "float64")) == 1e-10
+
+    # the explorer hands the bound to the evaluator only for random inputs
+    seen = []
+
+    class Module:
+        def get_evaluator(self, **kw):
+            seen.append(kw)
+            return type("E", (), {"evaluate": staticmethod(lambda: ([1e-3], 0, ""))})()
+
+    g = build_graph("matmul", [8, 8, 8], "float64")
+    for seed in (None, 3):
+        ex = Exploration(g, ExplorationConfig(backend="hip", random_inputs=seed, validate=True))
+        assert ex.evaluate_one(Module()) == ([1e-3], 0, "")
+    assert "scaled_tolerance" not in seen[0] and seen[1]["scaled_tolerance"] == 1e-10

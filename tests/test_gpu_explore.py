@@ -45,6 +45,17 @@ def test_loop_explore_c1_random_validated(tmp_path):
         assert r["backend"] == "hip"
 
 
+def test_loop_explore_random_inputs_validated(tmp_path):
+    """--random-inputs: every sample runs on the same seeded uniform[-1,1)
+    operands and is validated to max |diff| <= 1e-4 max |ref| (np.allclose's
+    atol would reject the fp32 rounding of near-zero outputs)."""
+    rows, recs, proc = _explore(tmp_path, "--search", "random", "--trials", "6", "--validate", "--random-inputs", "5")
+    assert len(recs) == 6 and all(r["results"][0] == 0 for r in recs), [r["error"] for r in recs]
+    assert len(rows) == 6
+    meta = json.loads(open(tmp_path / "e.csv.meta.json").read())
+    assert meta["args"]["random_inputs"] == 5 and meta["args"]["validate"] is True
+
+
 def test_loop_explore_c1_iterative(tmp_path):
     rows, recs, proc = _explore(tmp_path, "--search", "iterative", "--trials", "6", "--batch", "2", "--optimizer",
                                 "random-forest-default")

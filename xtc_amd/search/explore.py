@@ -52,7 +52,8 @@ import numpy as np
 from .strategies import Strategies
 
 __all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x", "OPERATORS",
-           "build_graph", "operation_dims", "config_graph", "random_parameters"]
+           "build_graph", "operation_dims", "config_graph", "random_parameters",
+           "random_inputs_tolerance"]
 
 logger = logging.getLogger("xtc_amd.search")
 
@@ -216,6 +217,16 @@ def random_parameters(graph: Any, seed: int) -> tuple[list[np.ndarray], list[np.
         ins.append(np.ascontiguousarray(x.astype(host_dtype(t.constant_dtype))))
     outs = [np.empty(tuple(t.constant_shape), dtype=host_dtype(t.constant_dtype)) for t in graph.outputs_types]
     return ins, outs
+
+
+def random_inputs_tolerance(graph: Any) -> float:
+    """Validation bound on random_parameters' inputs, as max |got - ref| /
+    max |ref|: the payload and numpy sum in different orders, so on
+    non-integer data they agree only to the accumulator's rounding.  1e-4
+    for fp32 accumulation (bf16 or fp32 operands: a wrong kernel is off by
+    O(1)), 1e-10 for float64."""
+    dtypes = {str(t.constant_dtype) for t in graph.outputs_types}
+    return 1e-10 if dtypes == {"float64"} else 1e-4
 
 
 def config_graph(config: ExplorationConfig) -> Any:
@@ -497,9 +508,12 @@ class Exploration:
     def evaluate_one(self, module: Any) -> tuple[list[float], int, str]:
         c = self.config
         check_explore_counters(c.pmu_counters)
+        extra = {}
+        if c.random_inputs is not None:
+            extra["scaled_tolerance"] = random_inputs_tolerance(self.graph if self.graph is not None else config_graph(c))
         return module.get_evaluator(
             repeat=c.repeat, number=c.number, min_repeat_ms=c.min_repeat_ms, validate=c.validate,
-            pmu_counters=self.counters(), parameters=c.eval_parameters,
+            pmu_counters=self.counters(), parameters=c.eval_parameters, **extra,
         ).evaluate()
 
     def split_counters(self, values: list[float]) -> tuple[list[float], dict[str, list[float]]]:
