@@ -549,6 +549,13 @@ def test_random_inputs_validate_to_a_scaled_bound():
     assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "bfloat16")) == 1e-4
     assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "float32")) == 1e-4
     assert random_inputs_tolerance(build_graph("matmul", [8, 8, 8], "float64")) == 1e-10
+    import xtc_amd.graphs.xtc.op as O
+
+    x = O.tensor((8, 8), "bfloat16", name="X")
+    y = O.tensor((8, 8), "bfloat16", name="Y")
+    with O.graph(name="mm_bf16_out") as gb:
+        O.matmul(x, y, name="Z")  # bf16 output: its rounding is coarser than the sums' differences
+    assert random_inputs_tolerance(gb.graph) == 1e-2
 
     # the explorer hands the bound to the evaluator only for random inputs
     seen = []

@@ -81,7 +81,7 @@ def main(argv: list[str] | None = None) -> int:
                    help="time (and validate) every sample on seeded uniform[-1,1) inputs, rounded to bfloat16 for "
                         "bfloat16 tensors, instead of the reference's np_init integers: on MI355X a bf16 GEMM's "
                         "clock depends on the power its operands draw. --validate then checks max |diff| <= "
-                        "1e-4 max |ref| (1e-10 for float64) in place of np.allclose")
+                        "1e-4 max |ref| (1e-10 for float64, 1e-2 for a bfloat16 output) in place of np.allclose")
     p.add_argument("--output", default="results.csv")
     p.add_argument("--db-file", help="output json db, for instance: xtc-graphs-db.json")
     _bool(p, "--resume", False, "skip samples already in --output")
