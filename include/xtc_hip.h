@@ -221,6 +221,15 @@ int xtc_hip_pad_f64(const double *x, double *y, int ndim, const int64_t *shape,
                     const int64_t *before, const int64_t *after, double value,
                     void *stream);
 
+/* Crop of a row-major tensor of rank <= 8 and elem_bytes-byte elements
+ * (2: bf16 words, 4: fp32, 8: fp64): shape is the input's, out has shape
+ * shape[d] - before[d] - after[d] and out[o] = x[o + before] (the slice of
+ * XTCOperUnpad.forward, operators.py:683-702; the subview copy of
+ * MlirOperatorUnpad, MlirOps.py:784-887).  A crop larger than its dim fails. */
+int xtc_hip_unpad(const void *x, void *y, int elem_bytes, int ndim,
+                  const int64_t *shape, const int64_t *before,
+                  const int64_t *after, void *stream);
+
 /* Round-to-nearest-even fp32 -> bf16 (stored as uint16) and back. */
 int xtc_hip_cast_f32_to_bf16(const float *x, uint16_t *y, uint64_t n, void *stream);
 int xtc_hip_cast_bf16_to_f32(const uint16_t *x, float *y, uint64_t n, void *stream);

@@ -19,6 +19,7 @@ __all__ = [
     "relu",
     "pad",
     "pad2d_padding",
+    "unpad",
     "round_bf16",
     "scaled_error",
     "seeded_uniform",
@@ -107,6 +108,17 @@ def pad(x: np.ndarray, pads: Sequence[tuple[int, int]], value: float = 0.0) -> n
     i.e. numpy.pad(mode="constant").
     """
     return np.pad(x, list(pads), mode="constant", constant_values=value)
+
+
+def unpad(x: np.ndarray, pads: Sequence[tuple[int, int]]) -> np.ndarray:
+    """Crop of per-axis (before, after) elements: the inverse of pad.
+
+    Follows XTCOperUnpad.forward (src/xtc/graphs/xtc/operators.py:683-702):
+    the slice [before : dim - after] on every axis.
+    """
+    if len(pads) != x.ndim:
+        raise ValueError("one (before, after) pair per axis")
+    return x[tuple(slice(lo, d - hi) for d, (lo, hi) in zip(x.shape, pads))].copy()
 
 
 def pad2d_padding(ndim: int, padding: int | tuple, axes: tuple[int, int] = (-3, -2)) -> list[tuple[int, int]]:

@@ -390,6 +390,53 @@ def test_pad_kernel_paths(shape, pads):
     np.testing.assert_array_equal(Y.to_numpy(expect.shape, np.float32), expect)
 
 
+_UNPAD_DT = {2: np.uint16, 4: np.float32, 8: np.float64}
+
+
+@pytest.mark.parametrize("shape,pads,elem", [
+    ((2, 9, 11, 64), [(0, 0), (1, 1), (2, 0), (0, 0)], 4),   # 16-byte row copies (innermost dim kept)
+    ((4, 8), [(3, 0), (1, 2)], 4),                           # element path
+    ((5, 6, 8), [(1, 1), (2, 1), (0, 0)], 2),                # bf16 words, rows of 16 bytes
+    ((3, 7, 5), [(0, 1), (1, 1), (1, 2)], 2),                # bf16 words, element path
+    ((6, 10), [(1, 2), (3, 3)], 8),                          # fp64, element path
+    ((4, 5, 6), [(1, 1), (0, 2), (0, 0)], 8),                # fp64, rows of 48 bytes
+    ((12,), [(0, 0)], 4),                                    # rank 1, nothing cropped: a copy
+    ((4, 3), [(2, 2), (0, 0)], 4),                           # empty output: nothing launched
+])
+def test_unpad_kernel_paths(shape, pads, elem):
+    """xtc_hip_unpad against the oracle's crop (XTCOperUnpad.forward), the
+    elements moved as raw words of their size: bit-exact."""
+    rng = np.random.default_rng(17)
+    dt = _UNPAD_DT[elem]
+    x = rng.integers(0, 2**15, shape).astype(dt) if elem == 2 else rng.uniform(-1, 1, shape).astype(dt)
+    expect = ref.unpad(x, pads)
+    X = DeviceBuffer.from_numpy(x)
+    Y = DeviceBuffer(max(expect.nbytes, 16))
+    nd = len(shape)
+    L = capi.lib()
+    capi.check(L.xtc_hip_unpad(X.c_ptr, Y.c_ptr, elem, nd, (ctypes.c_int64 * nd)(*shape),
+                               (ctypes.c_int64 * nd)(*[p[0] for p in pads]),
+                               (ctypes.c_int64 * nd)(*[p[1] for p in pads]), None))
+    capi.check(L.xtc_hip_synchronize())
+    if expect.size:
+        np.testing.assert_array_equal(Y.to_numpy(expect.shape, dt), expect)
+
+
+def test_unpad_rejects_bad_crops():
+    x = DeviceBuffer(4 * 24)
+    y = DeviceBuffer(4 * 24)
+    L = capi.lib()
+    shape = (ctypes.c_int64 * 2)(4, 6)
+    zero = (ctypes.c_int64 * 2)(0, 0)
+    with pytest.raises(capi.HipError, match="exceeds dim 1"):
+        capi.check(L.xtc_hip_unpad(x.c_ptr, y.c_ptr, 4, 2, shape, (ctypes.c_int64 * 2)(0, 4), (ctypes.c_int64 * 2)(0, 3),
+                                   None))
+    with pytest.raises(capi.HipError, match="element size 3"):
+        capi.check(L.xtc_hip_unpad(x.c_ptr, y.c_ptr, 3, 2, shape, zero, zero, None))
+    with pytest.raises(capi.HipError, match="negative"):
+        capi.check(L.xtc_hip_unpad(x.c_ptr, y.c_ptr, 4, 2, shape, (ctypes.c_int64 * 2)(-1, 0), zero, None))
+
+
 @pytest.mark.parametrize("offset", [0, 2])
 def test_cast_bf16_vector_and_unaligned(offset):
     # offset 0: 16-byte aligned, 8 elements per thread step plus a tail of 5;

@@ -134,6 +134,25 @@ def test_pad_layout():
     assert np.count_nonzero(p == -1.0) == p.size - x.size
 
 
+def test_unpad_inverts_pad_and_matches_an_index_loop():
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-1, 1, (3, 4, 5, 2))
+    pads = [(0, 1), (2, 0), (1, 3), (0, 0)]
+    # closed form: cropping what pad added gives the input back, whatever the pad value
+    np.testing.assert_array_equal(R.unpad(R.pad(x, pads, 7.0), pads), x)
+    # brute force on a tiny case: out[o] = in[o + before] per axis
+    y = rng.uniform(-1, 1, (4, 6))
+    got = R.unpad(y, [(1, 2), (3, 1)])
+    assert got.shape == (1, 2)
+    for i in range(1):
+        for j in range(2):
+            assert got[i, j] == y[i + 1, j + 3]
+    # a transposed operand or swapped before/after is caught
+    assert not np.array_equal(R.unpad(y, [(2, 1), (1, 3)]), got)
+    with pytest.raises(ValueError):
+        R.unpad(y, [(1, 1)])
+
+
 # ---------------------------------------------------------------- bf16 rounding
 
 def test_round_bf16_special_cases():

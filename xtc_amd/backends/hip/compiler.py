@@ -276,6 +276,16 @@ def _emit_launch(plan: Plan, ln: Launch, cfg: GemmConfig | SplitConfig | None, i
                 f"    if ((rc = xtc_hip_pad((const float *){_ptr(plan, ln.inputs[0])}, (float *){dst}, {nd}, s, b, e, "
                 f"{_c_float(a['value'])}, 0))) {{ record(rc, {where}); return; }} }}"
             )
+    elif ln.kind == "unpad":
+        nd = len(a["shape"])
+        shape = ", ".join(str(d) for d in a["shape"])
+        before = ", ".join(str(p[0]) for p in a["pads"])
+        after = ", ".join(str(p[1]) for p in a["pads"])
+        lines.append(f"  {{ static const int64_t s[{nd}] = {{{shape}}}, b[{nd}] = {{{before}}}, e[{nd}] = {{{after}}};")
+        lines.append(
+            f"    if ((rc = xtc_hip_unpad({_ptr(plan, ln.inputs[0])}, {dst}, {a['elem']}, {nd}, s, b, e, 0))) "
+            f"{{ record(rc, {where}); return; }} }}"
+        )
     elif ln.kind == "cast":
         lines.append(
             f"  if ((rc = xtc_hip_cast_f32_to_bf16((const float *){_ptr(plan, ln.inputs[0])}, (uint16_t *){dst}, "

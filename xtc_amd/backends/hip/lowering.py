@@ -11,8 +11,9 @@ HBM):
   * relu on a matmul/conv2d(/bias_add) result -> GEMM epilogue.
 A fusion happens only when the intermediate is used once and is not a graph
 output.  A matmul operand with layout [1, 0] (stored transposed) becomes the
-launch's trans_a / trans_b flag; other operators require natural layouts.  reshape is a view.  The reference lowers each node to its own
-linalg op (src/xtc/backends/mlir/MlirOps.py:166-782) and fuses only through
+launch's trans_a / trans_b flag; other operators require natural layouts.  reshape is a view; unpad
+is a crop kernel (16-byte row copies when the innermost dim is kept).  The reference lowers each node to its own
+linalg op (src/xtc/backends/mlir/MlirOps.py:166-887) and fuses only through
 transform-dialect producer fusion (MlirCompilerPasses.py:378-412).
 
 The plan uses only the graph interfaces (nodes, operation, inputs/outputs,
@@ -60,7 +61,7 @@ class Launch:
     """One kernel launch.  `node` is the scheduled node the launch serves
     (the matmul/conv2d for fused GEMMs); `absorbed` lists fused nodes."""
 
-    kind: str  # "matmul" | "conv2d" | "relu" | "pad" | "copy" | "cast"
+    kind: str  # "matmul" | "conv2d" | "relu" | "pad" | "unpad" | "copy" | "cast"
     node: str
     inputs: list[str]
     output: str
@@ -313,6 +314,23 @@ def lower_graph(graph: Any) -> Plan:
             attrs = {"shape": ishape, "pads": per, "value": float(op.attrs.get("constant_value", 0)), "dtype": dt}
             launches.append(Launch("pad", n.name, [n.inputs[0]], n.uid, attrs))
             scheduled[n.name] = n
+        elif name == "unpad":
+            # a crop: out[o] = in[o + before] per dim (operators.py:683-702)
+            dt = _dtype(t_out)
+            if dt not in (F32, F64, BF16):
+                raise UnsupportedGraph(f"unpad {n.name}: dtype {dt} is not supported")
+            ishape = _shape(out_type(n.inputs[0]))
+            padding = op.attrs.get("padding")
+            rank = len(ishape)
+            if isinstance(padding, dict):
+                per = [(0, 0)] * rank
+                for a, v in padding.items():
+                    per[a % rank] = (int(v[0]), int(v[1]))
+            else:
+                per = [(int(padding[0]), int(padding[1]))] * rank
+            attrs = {"shape": ishape, "pads": per, "elem": 2 if dt == BF16 else 8 if dt == F64 else 4}
+            launches.append(Launch("unpad", n.name, [n.inputs[0]], n.uid, attrs))
+            scheduled[n.name] = n
         elif name == "reshape":
             if n.uid in outputs:
                 launches.append(Launch("copy", n.name, [n.inputs[0]], n.uid, {}))
@@ -322,7 +340,7 @@ def lower_graph(graph: Any) -> Plan:
         else:
             raise UnsupportedGraph(
                 f"operator {name} ({n.name}) is not supported by the HIP backend "
-                "(supported: matmul, conv2d, relu, pad, pad2d, bias_add after matmul/conv2d, reshape)"
+                "(supported: matmul, conv2d, relu, pad, pad2d, unpad, bias_add after matmul/conv2d, reshape)"
             )
 
     # workspace layout: temps packed at 256-byte alignment

@@ -336,6 +336,44 @@ __global__ void pad_rows_kernel(const float4* __restrict__ x, float4* __restrict
   }
 }
 
+// Crop of a row-major tensor (unpad): out[o] = in[o + before] per dim, for
+// elements of T (2, 4 or 8 bytes; bf16 tensors move as their 16-bit words).
+// d.in_shape is the padded input, d.out_shape the cropped output.
+template <typename T>
+__global__ void unpad_kernel(const T* __restrict__ x, T* __restrict__ y, PadDims d, uint64_t total) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    uint64_t rem = i;
+    int64_t src = 0, src_stride = 1;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      const int64_t o = (int64_t)(rem % (uint64_t)d.out_shape[k]);
+      rem /= (uint64_t)d.out_shape[k];
+      src += (o + d.before[k]) * src_stride;
+      src_stride *= d.in_shape[k];
+    }
+    y[i] = x[src];
+  }
+}
+
+// Crop that keeps the innermost dim whole: 16-byte copies of its rows (the
+// row length in bytes and both pointers are multiples of 16).
+__global__ void unpad_rows_kernel(const uint4* __restrict__ x, uint4* __restrict__ y, PadDims d, uint64_t total16,
+                                  int64_t inner16) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total16; i += stride) {
+    uint64_t row = i / (uint64_t)inner16;
+    const int64_t col = (int64_t)(i - row * (uint64_t)inner16);
+    int64_t src = 0, src_stride = 1;
+    for (int k = d.ndim - 2; k >= 0; --k) {
+      const int64_t o = (int64_t)(row % (uint64_t)d.out_shape[k]);
+      row /= (uint64_t)d.out_shape[k];
+      src += (o + d.before[k]) * src_stride;
+      src_stride *= d.in_shape[k];
+    }
+    y[i] = x[src * inner16 + col];
+  }
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   unsigned u = __float_as_uint(f);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
@@ -2292,6 +2330,47 @@ int xtc_hip_pad_f64(const double* x, double* y, int ndim, const int64_t* shape, 
   if (total == 0) return 0;
   hipLaunchKernelGGL(pad_f64_kernel, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream), x, y, d, total,
                      value);
+  HIP_TRY(hipGetLastError());
+  return 0;
+}
+
+int xtc_hip_unpad(const void* x, void* y, int elem_bytes, int ndim, const int64_t* shape, const int64_t* before,
+                  const int64_t* after, void* stream) {
+  if (!current_state()) return fail("xtc_hip_init not called");
+  if (ndim < 1 || ndim > 8) return fail("unpad: rank %d unsupported", ndim);
+  if (elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return fail("unpad: element size %d unsupported", elem_bytes);
+  if (!x || !y || !shape || !before || !after) return fail("null operand");
+  PadDims d;
+  memset(&d, 0, sizeof(d));
+  d.ndim = ndim;
+  uint64_t total = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (shape[k] < 0 || before[k] < 0 || after[k] < 0) return fail("unpad: negative extent");
+    if (before[k] + after[k] > shape[k])
+      return fail("unpad: crop %lld + %lld exceeds dim %d of size %lld", (long long)before[k], (long long)after[k], k,
+                  (long long)shape[k]);
+    d.in_shape[k] = shape[k];
+    d.before[k] = before[k];
+    d.out_shape[k] = shape[k] - before[k] - after[k];
+    total *= (uint64_t)d.out_shape[k];
+  }
+  if (total == 0) return 0;
+  const int last = ndim - 1;
+  const int64_t row_bytes = shape[last] * elem_bytes;
+  if (before[last] == 0 && after[last] == 0 && row_bytes % 16 == 0 && aligned16(x) && aligned16(y)) {
+    const uint64_t total16 = total * (uint64_t)elem_bytes / 16;
+    hipLaunchKernelGGL(unpad_rows_kernel, dim3(grid_for(total16, 256)), dim3(256), 0, pick_stream(stream),
+                       (const uint4*)x, (uint4*)y, d, total16, row_bytes / 16);
+  } else if (elem_bytes == 2) {
+    hipLaunchKernelGGL(unpad_kernel<uint16_t>, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
+                       (const uint16_t*)x, (uint16_t*)y, d, total);
+  } else if (elem_bytes == 4) {
+    hipLaunchKernelGGL(unpad_kernel<uint32_t>, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
+                       (const uint32_t*)x, (uint32_t*)y, d, total);
+  } else {
+    hipLaunchKernelGGL(unpad_kernel<uint64_t>, dim3(grid_for(total, 256)), dim3(256), 0, pick_stream(stream),
+                       (const uint64_t*)x, (uint64_t*)y, d, total);
+  }
   HIP_TRY(hipGetLastError());
   return 0;
 }

@@ -398,7 +398,7 @@ class XTCOperPad2D(_PadSemantics, XTCOperator):
 
 
 class XTCOperUnpad(_PadSemantics, XTCOperator):
-    """Crops what a pad added (operators.py:594-690)."""
+    """Crops what a pad added (operators.py:594-702)."""
 
     sign = -1
 

@@ -175,6 +175,19 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             _vp,
         ],
     ),
+    "xtc_hip_unpad": (
+        _i,
+        [
+            _vp,
+            _vp,
+            _i,
+            _i,
+            ctypes.POINTER(ctypes.c_int64),
+            ctypes.POINTER(ctypes.c_int64),
+            ctypes.POINTER(ctypes.c_int64),
+            _vp,
+        ],
+    ),
     "xtc_hip_cast_f32_to_bf16": (_i, [_vp, _vp, _u64, _vp]),
     "xtc_hip_cast_bf16_to_f32": (_i, [_vp, _vp, _u64, _vp]),
     "xtc_hip_matmul_desc_size": (_i, []),
