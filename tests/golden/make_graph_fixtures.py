@@ -9,9 +9,10 @@ tests/golden/graph_prints.json as {test name: [pattern lines]} (data only).
 Also reads /root/reference/tests/filecheck/backends/padding/test_*.py (pad,
 pad2d and unpad around matmul and conv2d) and keeps, per test, the printed
 graph its CHECK lines expect (from `graph:` to the first blank line) and
-whether it expects the validated run to end with `CODE: 0`.  Writes
+whether it expects the validated run to end with `CODE: 0`, and the error
+that backends/invalid/test_pad2d_invalid.py expects.  Writes
 tests/golden/padding_graph_prints.json as {test name: {"graph": [lines],
-"code0": bool}} (data only).
+"code0": bool}} plus {"test_pad2d_invalid": {"error": line}} (data only).
 
 Run once in the build container; the fixtures are committed.
 """
@@ -25,6 +26,7 @@ from pathlib import Path
 SRC = Path("/root/reference/tests/filecheck/graphs")
 OUT = Path(__file__).resolve().parent / "graph_prints.json"
 PAD_SRC = Path("/root/reference/tests/filecheck/backends/padding")
+PAD_INVALID = Path("/root/reference/tests/filecheck/backends/invalid/test_pad2d_invalid.py")
 PAD_OUT = Path(__file__).resolve().parent / "padding_graph_prints.json"
 
 
@@ -41,6 +43,8 @@ def padding_prints() -> dict:
         start = pats.index("graph:")
         end = pats.index("", start) if "" in pats[start:] else len(pats)
         out[path.stem] = {"graph": pats[start:end], "code0": "CODE: 0" in pats}
+    # the expected error of the invalid pad2d test: "<exception>: <message>"
+    out[PAD_INVALID.stem] = {"error": [p.strip() for p in _patterns(PAD_INVALID)][0]}
     return out
 
 

@@ -4,7 +4,7 @@ padding tests (tests/filecheck/backends/padding/test_*.py).
 
 tests/golden/padding_graph_prints.json holds, per reference test, the graph
 print its FileCheck lines expect and whether its validated run ends with
-`CODE: 0`.  Each case here builds the same graph with xtc_amd's DSL (the
+`CODE: 0`, and the error backends/invalid/test_pad2d_invalid.py expects.  Each case here builds the same graph with xtc_amd's DSL (the
 same calls and argument forms as the reference test), matches the print on
 the CPU, checks the launch plan, and on the GPU compiles it with the
 reference test's scheduler choice and runs the executor with validate=True
@@ -27,7 +27,9 @@ import xtc_amd.graphs.xtc.op as O
 from oracle import reference as R
 
 ROOT = Path(__file__).resolve().parent.parent
-PRINTS = json.loads((Path(__file__).parent / "golden" / "padding_graph_prints.json").read_text())
+_FIXTURE = json.loads((Path(__file__).parent / "golden" / "padding_graph_prints.json").read_text())
+INVALID = _FIXTURE.pop("test_pad2d_invalid")["error"]
+PRINTS = _FIXTURE
 
 N, H, W, F, RR, S, C, SH, SW = 1, 8, 8, 16, 5, 5, 3, 2, 2
 I_, J_, K_ = 14, 14, 14
@@ -110,6 +112,19 @@ def _match(output: str, patterns: list[str]) -> None:
 def test_every_reference_padding_test_has_a_builder():
     assert {_base(k) for k in PRINTS} == set(BUILDERS)
     assert len(PRINTS) == 18 and all(v["code0"] for v in PRINTS.values())
+
+
+def test_invalid_pad2d_padding_reports_the_reference_message():
+    """backends/invalid/test_pad2d_invalid.py: a one-axis dict for pad2d.
+    The reference fails an assert; this DSL raises ValueError with the same
+    text."""
+    exc_name, message = INVALID.split(": ", 1)
+    assert exc_name == "AssertionError"
+    a = O.tensor((I_, K_), "float32", name="A")
+    with pytest.raises(ValueError) as info:
+        with O.graph(name="pad_matmul_unpad"):
+            O.pad2d(a, padding={-2: 2}, name="A_pad")
+    assert str(info.value) == message
 
 
 @pytest.fixture(scope="module")

@@ -332,7 +332,7 @@ class XTCOperPad(_PadSemantics, XTCOperator):
         padding = attrs.get("padding", 0)
         value = attrs.get("constant_value", 0)
         if not isinstance(value, (int, float)):
-            raise ValueError("constant_value must be a number")
+            raise ValueError("constant_value need to be a number")  # the reference's message (operators.py:461)
         if isinstance(padding, int):
             padding = (padding, padding)
         elif isinstance(padding, (tuple, list)) and len(padding) == 2 and all(isinstance(p, int) for p in padding):
@@ -343,7 +343,7 @@ class XTCOperPad(_PadSemantics, XTCOperator):
         elif isinstance(padding, dict):
             padding = {k: (v, v) if isinstance(v, (int, float)) else tuple(v) for k, v in padding.items()}
         else:
-            raise ValueError("padding is an int, a pair, a sequence or a dict")
+            raise ValueError("padding is either a list of tuple/int or int or a dict")
         if isinstance(padding, dict):
             padding = {k: v for k, v in padding.items() if v != (0, 0)}
         super().__init__("pad", device=attrs.get("device"), padding=padding, constant_value=value)
@@ -366,16 +366,21 @@ class XTCOperPad2D(_PadSemantics, XTCOperator):
         padding = attrs.get("padding", (0, 0, 0, 0))
         value = attrs.get("constant_value", 0)
         axes = tuple(attrs.get("axes", (-3, -2)))
-        if len(axes) != 2 or axes[0] == axes[1]:
-            raise ValueError(f"pad2d needs two different axes: {axes}")
+        # the error texts are the reference's assertion messages (operators.py:514-553)
+        if len(axes) != 2:
+            raise ValueError(f"axes for pad2d of wrong size, expected 2: {axes}")
+        if axes[0] == axes[1]:
+            raise ValueError(f"axes need 2 different dimension to pad: {axes}")
         if not isinstance(value, (int, float)):
-            raise ValueError("constant_value must be a number")
+            raise ValueError("constant_value need to be a number")
+        if not isinstance(padding, (int, tuple, list, dict)):
+            raise ValueError(f"padding for pad2d of wrong type, expect int or tuple or dict: {padding}")
         a0, a1 = axes
         if isinstance(padding, int):
             norm = {a0: (padding, padding), a1: (padding, padding)}
         elif isinstance(padding, dict):
             if len(padding) != 2:
-                raise ValueError("pad2d padding dict must name two axes")
+                raise ValueError(f"padding for pad2d of wrong size, expected 1, 2 or 4: {padding}")
             norm = {k: (v, v) if isinstance(v, int) else tuple(v) for k, v in padding.items()}
         elif isinstance(padding, (tuple, list)) and len(padding) == 1:
             norm = {a0: (padding[0], padding[0]), a1: (padding[0], padding[0])}
@@ -386,7 +391,7 @@ class XTCOperPad2D(_PadSemantics, XTCOperator):
         elif isinstance(padding, (tuple, list)) and len(padding) == 4:
             norm = {a0: (padding[0], padding[1]), a1: (padding[2], padding[3])}
         else:
-            raise ValueError(f"pad2d padding must have 1, 2 or 4 entries: {padding}")
+            raise ValueError(f"padding for pad2d of wrong size, expected 1, 2 or 4: {padding}")
         norm = {k: v for k, v in norm.items() if v != (0, 0)}
         super().__init__("pad2d", device=attrs.get("device"), padding=norm, constant_value=value)
 
