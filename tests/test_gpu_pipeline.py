@@ -240,6 +240,28 @@ def test_unfused_pad_and_relu_kernels():
     np.testing.assert_array_equal(r_out, np.maximum(c_out, 0.25))
 
 
+def test_ndarray_parameters_on_the_device():
+    """NDArray (runtimes/types/ndarray.py:23-237) with the HIP device as its
+    runtime holds its tensor in HBM; an evaluator takes NDArrays as
+    parameters and writes the payload's outputs back into them."""
+    from xtc_amd.runtimes.hip.device import HipDevice
+    from xtc_amd.runtimes.types.ndarray import NDArray
+
+    rng = np.random.default_rng(8)
+    a = rng.uniform(-1, 1, (64, 96)).astype(np.float32)
+    b = rng.uniform(-1, 1, (96, 32)).astype(np.float32)
+    dev = HipDevice()
+    na, nb = NDArray(a, runtime=dev), NDArray(b, runtime=dev)
+    nc = NDArray(np.zeros((64, 32), np.float32), runtime=dev)
+    assert na.is_on_device() and na.data.value != a.ctypes.data and np.array_equal(na.numpy(), a)
+    module = _compile(_matmul_graph(64, 32, 96, "float32"))
+    _, code, msg = module.get_evaluator(parameters=([na, nb], [nc]), repeat=1, number=1, min_repeat_ms=0).evaluate()
+    assert code == 0, msg
+    assert ref.scaled_error(nc.numpy(), ref.matmul(a, b), 96, 1.0, 1.0) <= TOL_F32
+    t = NDArray(a, runtime=dev, layout=[1, 0])  # stored transposed in HBM, read back logical
+    assert t.shape == (96, 64) and np.array_equal(t.numpy(), a)
+
+
 def test_bias_add_epilogue():
     rng = np.random.default_rng(4)
     a = rng.uniform(-1, 1, (96, 64)).astype(np.float32)

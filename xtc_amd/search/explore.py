@@ -33,7 +33,6 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import csv
-import hashlib
 import json
 import logging
 import os
@@ -49,9 +48,11 @@ from typing import Any, Callable
 
 import numpy as np
 
+from .callback import DB_VERSION, CSVCallback, DBCallback, MemoryCallback, ResultCallBack, db_operator, db_strategy
 from .strategies import Strategies
 
-__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "hip_sample_filter", "parse_x", "OPERATORS",
+__all__ = ["ExplorationConfig", "Exploration", "CSVCallback", "DBCallback", "MemoryCallback", "ResultCallBack",
+           "hip_sample_filter", "parse_x", "OPERATORS",
            "build_graph", "operation_dims", "config_graph", "random_parameters",
            "random_inputs_tolerance"]
 
@@ -252,102 +253,9 @@ def config_graph(config: ExplorationConfig) -> Any:
     return build_graph(config.operator, dims, config.dtype, config.pad, name=config.func_name or config.operator)
 
 
-class CSVCallback:
-    """Writes one row per successful sample; `resume` skips (backend, sample)
-    pairs already in the file, `append` appends without a new header."""
-
-    def __init__(self, fname: str, peak_time: float, sample_names: list[str], *, resume: bool = False,
-                 append: bool = False) -> None:
-        self._fname = fname
-        self._peak_time = peak_time
-        self._names = sample_names
-        self.seen: set[tuple[str, tuple[int, ...]]] = set()
-        path = Path(fname)
-        existing = path.exists() and path.stat().st_size > 0
-        if resume and existing:
-            with open(path, newline="") as f:
-                for row in csv.DictReader(f):
-                    try:
-                        self.seen.add((row["backend"], tuple(int(row[n]) for n in self._names)))
-                    except (KeyError, TypeError, ValueError):
-                        continue
-        mode = "a" if (resume or append) else "w"
-        self._f = open(path, mode, newline="")
-        self._w = csv.writer(self._f)
-        if mode == "w" or not existing:
-            self._w.writerow(self._names + ["X", "time", "peak", "backend"])
-            self._f.flush()
-
-    def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str) -> None:
-        if code != 0 or not times:
-            return
-        key = (backend, tuple(int(v) for v in sample))
-        if key in self.seen:
-            return
-        t = min(times)
-        # X keeps the sample in one field: list separators become ';'
-        x = str([int(v) for v in sample]).replace(",", ";")
-        self._w.writerow([*sample, x, t, self._peak_time / t if t > 0 else 0.0, backend])
-        self._f.flush()
-        self.seen.add(key)
-
-    def close(self) -> None:
-        self._f.close()
-
-
 def parse_x(text: str) -> list[int]:
     """The X column back to a sample ('[1; 2; 3]' or '[1, 2, 3]')."""
     return [int(v) for v in json.loads(text.replace(";", ","))]
-
-
-DB_VERSION = "v0.2"
-
-
-def db_operator(graph: Any) -> list[Any]:
-    """["xtc.graph", sha1 of the graph dict without its name, the dict]."""
-    obj = graph.to_dict()
-    obj.pop("name", None)
-    return ["xtc.graph", hashlib.sha1(json.dumps(obj).encode()).hexdigest(), obj]
-
-
-def db_strategy(name: str) -> list[Any]:
-    return ["xtc.strategy", hashlib.sha1(json.dumps(name).encode()).hexdigest(), name]
-
-
-class DBCallback:
-    """One JSON line per sample in the results-DB record format of the
-    reference (version, platform, compiler, operator, strategy, schedule,
-    results=[code, [seconds]]; src/xtc/search/callback.py:25-66,
-    src/xtc/cli/query_results.py:25-123); a failed sample records time 0.
-    `kernels` (the kernel instance of each scheduled node) is extra."""
-
-    def __init__(self, fname: str, graph: Any, strategy: str, target: str = "gfx950", threads: int = 1) -> None:
-        from .. import __version__
-
-        self._f = open(fname, "a")
-        self._operator = db_operator(graph)
-        self._strategy = db_strategy(strategy)
-        self._platform = [platform.node().split(".")[0], platform.system(), platform.machine()]
-        self._compiler = ["xtc", "v" + __version__, target, threads]
-
-    def __call__(self, sample: list[int], backend: str, times: list[float], code: int, msg: str,
-                 extra: dict[str, Any] | None = None) -> None:
-        t = min(times) if (code == 0 and times) else 0.0
-        rec = {
-            "version": [DB_VERSION],
-            "platform": self._platform,
-            "compiler": [*self._compiler, backend],
-            "operator": self._operator,
-            "strategy": self._strategy,
-            "schedule": [int(v) for v in sample],
-            "results": [int(code), [float(t)]],
-            **(extra or {}),
-        }
-        self._f.write(json.dumps(rec) + "\n")
-        self._f.flush()
-
-    def close(self) -> None:
-        self._f.close()
 
 
 def hip_sample_filter(graph: Any, strategy_factory: Callable[..., Any]) -> Callable[[list[int]], bool]:
@@ -583,9 +491,13 @@ class Exploration:
             times, code, msg = [], 2, f"{type(err).__name__}: {err}"
         if code:
             logger.warning("sample %s failed: %s", sample, msg)
-        csv_cb(sample, c.backend, times, code, msg)
+        if code == 0 and not times:
+            code, msg = 2, "the evaluator returned no time"
+        # the callbacks' result tuple (src/xtc/search/callback.py): time is the minimum over the repeats
+        result = (sample, code, min(times) if code == 0 else 0.0, c.backend)
+        csv_cb(result)
         if db_cb:
-            db_cb(sample, c.backend, times, code, msg, {**extra, "error": msg})
+            db_cb.record(result, {**extra, "error": msg})
         return (sample, times, code, msg)
 
     def _run_batch(
@@ -659,7 +571,10 @@ class Exploration:
                 Path(c.save_temps_dir).mkdir(parents=True, exist_ok=True)
                 self.graph.dump(str(Path(c.save_temps_dir) / f"{self.graph.name}.graph.yaml"))
             csv_cb = CSVCallback(c.output, peak_time, self.strategy.sample_names, resume=c.resume, append=c.append)
-            db_cb = DBCallback(c.db_file, self.graph, "descript" if c.descript else self.strategy_name(c.strategy)) if c.db_file else None
+            db_cb = None
+            if c.db_file:
+                db_cb = DBCallback(c.db_file, "gfx950", 1, "descript" if c.descript else self.strategy_name(c.strategy))
+                db_cb.set_graph(self.graph)
             try:
                 with cf.ThreadPoolExecutor(max_workers=max(1, c.jobs)) as pool:
                     if iterative:

@@ -8,11 +8,13 @@ HostEvaluator (src/xtc/targets/host/HostEvaluator.py:28-120):
   init_zero=False, pmu_counters=[], np_inputs_spec, np_outputs_spec,
   reference_impl.
 Steps: init device -> load payload -> inputs (np_init integers 1..9 unless
-`parameters`) copied to HBM -> optional validation against the graph's numpy
-interpreter with np.allclose (src/xtc/utils/evaluation.py:129-145) ->
-timing with the evaluate_perf protocol -> unload -> copy outputs back into
-caller-provided arrays.  Returns (per-repeat seconds per call, code, msg);
-code 1 on a validation mismatch, 2 on a HIP/payload error.
+`parameters`: numpy arrays or NDArrays, on the host or the device) copied
+to HBM -> optional validation against the graph's numpy interpreter with
+np.allclose (src/xtc/utils/evaluation.py:129-145) -> timing with the
+evaluate_perf protocol -> unload -> copy outputs back into caller-provided
+arrays (numpy arrays, or NDArrays through copy_from_numpy).  Returns
+(per-repeat seconds per call, code, msg); code 1 on a validation mismatch,
+2 on a HIP/payload error.
 With pmu_counters the results are, per repeat, one value per counter, per
 call (src/xtc/csrcs/runtimes/host/evaluate_perf.c:63-125): "gpu.time" /
 "gpu.clocks" from HIP events, "gpu.cycles" and "gpu.<counter>" from the
@@ -184,6 +186,8 @@ class HipEvaluator(Evaluator):
                 for dst, d in zip(self._parameters[1], d_outs):
                     if isinstance(dst, np.ndarray):
                         d.numpy(out=dst)
+                    elif hasattr(dst, "copy_from_numpy"):  # an NDArray (xtc_amd.runtimes.types)
+                        dst.copy_from_numpy(d.numpy())
         except capi.HipError as err:
             result = ([], 2, f"Error in execution: {err}")
         finally:

@@ -5,6 +5,8 @@ from __future__ import annotations
 
 from collections.abc import Callable, Hashable, Iterator
 
+from .math import estimate_unique_prob_good_turing
+
 __all__ = ["sample_uniques"]
 
 
@@ -16,7 +18,8 @@ def sample_uniques(draw: Callable[[int], Iterator[Hashable]], num: int, prob: fl
     round).  The stop test estimates the chance that the next request yields
     a new unique sample as P(valid) * P(unseen), with P(valid) the fraction
     of requests that produced a candidate and P(unseen) the smoothed
-    Good-Turing estimate (singletons + 1) / (draws + 1).  The stream of
+    Good-Turing estimate (singletons + 1) / (draws + 1)
+    (estimate_unique_prob_good_turing).  The stream of
     accepted samples is the reference's, so seeded explorations agree.
     """
     round_num = num
@@ -41,7 +44,7 @@ def sample_uniques(draw: Callable[[int], Iterator[Hashable]], num: int, prob: fl
             elif s in twice:
                 twice.remove(s)
         p_valid = max(1 / (requests + 1), draws / requests)
-        p_unseen = (len(once) + 1) / (draws + 1)
+        p_unseen = estimate_unique_prob_good_turing(draws, len(once))
         p_next = p_valid * p_unseen
         if not got:
             round_num *= 2

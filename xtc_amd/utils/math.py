@@ -1,5 +1,6 @@
 # SPDX-License-Identifier: BSD-3-Clause
-"""Integer helpers of the tiling search (src/xtc/utils/math.py:13-95)."""
+"""Integer helpers of the tiling search (src/xtc/utils/math.py:13-95) and
+the sample-space estimators of its unique sampling (math.py:103-158)."""
 
 from __future__ import annotations
 
@@ -13,6 +14,9 @@ __all__ = [
     "sizes_to_factors",
     "mulall",
     "pow2divisor",
+    "estimate_count_prob_smooth",
+    "estimate_unique_prob_good_turing",
+    "estimate_unique_num_chao1",
 ]
 
 
@@ -80,3 +84,34 @@ def mulall(args: list[int]) -> int:
 def pow2divisor(value: int) -> int:
     """Largest power of two dividing value."""
     return value & -value
+
+
+def estimate_count_prob_smooth(count: int, sample_size: int, alpha: float = 1.0) -> float:
+    """Additive (Laplace) smoothing of the frequency count / sample_size:
+    (count + alpha) / (sample_size + alpha), and 0 for alpha = 0 with no
+    samples (math.py:141-158)."""
+    if not 0 <= count <= sample_size or alpha < 0:
+        raise ValueError(f"need 0 <= count <= sample_size and alpha >= 0: {count}, {sample_size}, {alpha}")
+    if alpha == 0 and sample_size == 0:
+        return 0.0
+    return (count + alpha) / (sample_size + alpha)
+
+
+def estimate_unique_prob_good_turing(sample_size: int, once_num: int) -> float:
+    """Good-Turing estimate of the chance that the next draw is a value not
+    seen yet: the share of draws seen exactly once, smoothed as above so
+    that empty or small samples give a usable value (math.py:126-138)."""
+    if not 0 <= once_num <= sample_size:
+        raise ValueError(f"need 0 <= once_num <= sample_size: {once_num}, {sample_size}")
+    return estimate_count_prob_smooth(once_num, sample_size)
+
+
+def estimate_unique_num_chao1(unique_num: int, once_num: int, twice_num: int) -> int:
+    """Bias-corrected Chao1 lower bound on the number of distinct values of a
+    space, from the distinct values drawn so far and those seen exactly once
+    (f1) and twice (f2): S_obs + f1 (f1 - 1) / (2 (f2 + 1)), rounded to the
+    nearest integer (Chao's estimator as the SpadeR guide states it;
+    math.py:103-123)."""
+    if once_num < 0 or twice_num < 0 or unique_num < once_num + twice_num:
+        raise ValueError(f"need f1, f2 >= 0 and unique_num >= f1 + f2: {unique_num}, {once_num}, {twice_num}")
+    return int(unique_num + once_num * (once_num - 1) / (2 * (twice_num + 1)) + 0.5)
