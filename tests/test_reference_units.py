@@ -285,3 +285,55 @@ def test_interface_modules():
     for abc in (Backend, Compiler, Tensor, TensorType, Graph, Node, Operator, Schedule, Scheduler):
         with pytest.raises(TypeError):
             abc()
+
+
+# ------------------------------------------- pytest/graphs/test_graph_serialization.py
+
+def test_graph_serialization_round_trips(tmp_path):
+    import xtc_amd.graphs.xtc.op as O
+
+    golden = Path(__file__).parent / "golden" / "graphs"
+    for name in ("matmul", "conv2d"):
+        with O.graph() as gb:
+            gb.load(golden / f"{name}.graph.yaml")
+        assert gb.graph.name == name
+    # dict, string and file round trips
+    a, b = O.tensor((4, 512), "float32", name="A"), O.tensor((512, 32), "float32", name="B")
+    with O.graph(name="matmul_relu") as gb:
+        O.relu(O.matmul(a, b, name="matmul"), name="relu")
+    d = gb.graph.to_dict()
+    with O.graph() as gb2:
+        gb2.from_dict(d)
+    assert d and d == gb2.graph.to_dict()
+    i, w = O.tensor((1, 8, 8, 3), "float32", name="I"), O.tensor((5, 5, 3, 16), "float32", name="W")
+    with O.graph(name="pad_conv2d_nhwc_mini") as gb:
+        O.conv2d(O.pad(i, padding={1: 2, 2: (2, 2)}, name="pad"), w, stride=(2, 2), name="conv")
+    text = gb.graph.dumps()
+    with O.graph(name="other") as gb2:
+        gb2.loads(text)
+    assert text and text == gb2.graph.dumps()
+    gb.graph.dump(str(tmp_path / "g.yaml"))
+    with O.graph() as gb3:
+        gb3.load(str(tmp_path / "g.yaml"))
+    assert gb.graph.to_dict() == gb3.graph.to_dict()
+    # nested subgraphs and an output chosen by the user survive the dict form
+    ts = [O.tensor() for _ in range(5)]
+
+    def fc(x, wt, n):
+        return O.matmul(O.reshape(x, shape=(1, -1)), O.reshape(wt, shape=(-1, n)))
+
+    with O.graph(name="mlp4") as gb:
+        with O.graph(name="l1"):
+            l1 = O.relu(fc(ts[0], ts[1], 512))
+        with O.graph(name="l2"):
+            l2 = O.relu(fc(l1, ts[2], 256))
+        with O.graph(name="l3"):
+            l3 = O.relu(fc(l2, ts[3], 128))
+        with O.graph(name="l4"):
+            l4 = fc(l3, ts[4], 10)
+        O.reshape(l4, shape=(-1,))
+        O.outputs(l1)
+    d = gb.graph.to_dict()
+    with O.graph() as gb2:
+        gb2.from_dict(d)
+    assert d and d == gb2.graph.to_dict()
