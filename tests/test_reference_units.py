@@ -1,9 +1,10 @@
 # SPDX-License-Identifier: BSD-3-Clause
-"""The reference's unit tests (tests/pytest/unit/*), replayed on this
-package's restatements: the sample-space estimators and unique sampling of
-the search, the result callbacks, the compile/execute pipeline, the
-NDArray runtime type and the interface modules.  The input/expected values
-are the reference tests' own; the test code is this package's.
+"""The reference's unit tests (tests/pytest/unit/*, tests/pytest/graphs/),
+replayed on this package's restatements: the sample-space estimators and
+unique sampling of the search, the result callbacks, the compile/execute
+pipeline, the NDArray runtime type, the interface modules and graph
+serialization.  The input/expected values are the reference tests' own;
+the test code is this package's.
 """
 
 from __future__ import annotations
