@@ -283,7 +283,13 @@ def test_interface_modules():
     from xtc_amd.itf.schd.schedule import Schedule
     from xtc_amd.itf.schd.scheduler import Scheduler
 
-    for abc in (Backend, Compiler, Tensor, TensorType, Graph, Node, Operator, Schedule, Scheduler):
+    from xtc_amd.itf.exec.evaluator import Evaluator
+    from xtc_amd.itf.exec.executor import Executor
+    from xtc_amd.itf.search.optimizer import Optimizer
+    from xtc_amd.itf.search.strategy import Strategy
+
+    for abc in (Backend, Compiler, Tensor, TensorType, Graph, Node, Operator, Schedule, Scheduler, Evaluator,
+                Executor, Strategy, Optimizer):
         with pytest.raises(TypeError):
             abc()
 

@@ -1,65 +1,7 @@
 # SPDX-License-Identifier: BSD-3-Clause
-"""Strategy and Optimizer interfaces (src/xtc/itf/search/strategy.py:22-164,
-src/xtc/itf/search/optimizer.py)."""
+"""Strategy and Optimizer interfaces (src/xtc/itf/search/)."""
 
-from __future__ import annotations
-
-from abc import ABC, abstractmethod
-from collections.abc import Iterator
-from typing import TYPE_CHECKING, Any, TypeAlias
-
-if TYPE_CHECKING:
-    from ..graph import Graph
-    from ..schd.scheduler import Scheduler
+from .optimizer import Optimizer, VecSample
+from .strategy import Sample, Strategy
 
 __all__ = ["Sample", "VecSample", "Strategy", "Optimizer"]
-
-Sample: TypeAlias = Any
-VecSample: TypeAlias = "list[int]"
-
-
-class Strategy(ABC):
-    """A schedule search space over one graph.
-
-    A sample is a point of the space; `generate(scheduler, sample)` applies
-    the corresponding transformations to a Scheduler.
-    """
-
-    @property
-    @abstractmethod
-    def graph(self) -> "Graph": ...
-
-    @abstractmethod
-    def generate(self, scheduler: "Scheduler", sample: Sample) -> None: ...
-
-    @abstractmethod
-    def exhaustive(self) -> Iterator[Sample]: ...
-
-    @abstractmethod
-    def sample(self, num: int, seed: int | None = 0) -> Iterator[Sample]: ...
-
-    @abstractmethod
-    def default_schedule(self, opt_level: int = 2) -> Sample: ...
-
-    @property
-    @abstractmethod
-    def sample_names(self) -> list[str]: ...
-
-    @abstractmethod
-    def dict_to_sample(self, sample: dict[str, Any]) -> Sample: ...
-
-    @abstractmethod
-    def sample_to_dict(self, sample: Sample) -> dict[str, int]: ...
-
-
-class Optimizer(ABC):
-    """Suggest/observe loop of an iterative search."""
-
-    @abstractmethod
-    def suggest(self) -> list[VecSample]: ...
-
-    @abstractmethod
-    def observe(self, x: list[VecSample], y: list[float]) -> None: ...
-
-    @abstractmethod
-    def finished(self) -> bool: ...
