@@ -570,3 +570,20 @@ def test_random_inputs_validate_to_a_scaled_bound():
         ex = Exploration(g, ExplorationConfig(backend="hip", random_inputs=seed, validate=True))
         assert ex.evaluate_one(Module()) == ([1e-3], 0, "")
     assert "scaled_tolerance" not in seen[0] and seen[1]["scaled_tolerance"] == 1e-10
+
+
+def test_exploration_static_helpers(capsys):
+    """The reference's Exploration static API (explore.py:211-261, 813-862):
+    graph builders with its tensor names, listings, named-operation dims."""
+    g = Exploration.xtc_matmul_graph(4, 32, 512, "float32")
+    assert [str(t) for t in g.inputs_types] == ["4x512xfloat32", "512x32xfloat32"] and g.name == "matmul"
+    assert [str(t) for t in Exploration.xtc_conv2d_graph(1, 4, 4, 16, 5, 5, 3, 2, 2, "float32").outputs_types] == [
+        "1x4x4x16xfloat32"]
+    assert [str(t) for t in Exploration.xtc_relu_graph(10, "float64").inputs_types] == ["10xfloat64"]
+    Exploration.list_operators()
+    Exploration.list_optimizers()
+    Exploration.list_strategies()
+    out = capsys.readouterr().out.split()
+    assert out[:3] == ["matmul", "conv2d", "relu"] and "random-forest-default" in out and "tile_hip" in out
+    assert Exploration.get_operation_dims("conv2d", "ResNet18_01") == [1, 224, 224, 64, 7, 7, 3, 2, 2]
+    assert Exploration.get_strategy_name("tile_oo") == "tile_oo"

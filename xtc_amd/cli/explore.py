@@ -30,7 +30,6 @@ import sys
 from typing import Any
 
 from ..search.explore import OPERATORS, Exploration, ExplorationConfig, build_graph, operation_dims
-from ..search.strategies import Strategies
 
 # default dims of the reference's OPERATORS table (src/xtc/search/explore.py:151-198)
 DEFAULT_DIMS = {name: list(op["default_dims"]) for name, op in OPERATORS.items()}
@@ -128,19 +127,13 @@ def main(argv: list[str] | None = None) -> int:
         print("\n".join(DEFAULT_DIMS))
         return 0
     if args.op_name_list:
-        from ..artifacts import get_operation, list_operations
-
-        for _, name in list_operations(args.operator):
-            op = get_operation(args.operator, name)
-            print(f"{name}: {op['dims']}, {op['params']}")
+        Exploration.list_operations_dims(args.operator)
         return 0
     if args.strategy_list:
-        print("\n".join(Strategies.names(include_aliases=True)))
+        Exploration.list_strategies()
         return 0
     if args.optimizer_list:
-        from ..search.optimizers import Optimizers
-
-        print("\n".join(Optimizers.names()))
+        Exploration.list_optimizers()
         return 0
     if args.pmu_counters:
         from ..search.explore import check_explore_counters

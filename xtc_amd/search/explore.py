@@ -339,6 +339,61 @@ class Exploration:
         self.strategy = factory(**kwargs)
         self.peak_time_s = 0.0  # the graph's time at peak, set by run()
 
+    # ---- the reference's static helpers (src/xtc/search/explore.py:211-261, 813-862)
+    @staticmethod
+    def xtc_load_graph(graph_file: str) -> Any:
+        import xtc_amd.graphs.xtc.op as O
+
+        with O.graph() as gb:
+            gb.load(graph_file)
+        return gb.graph
+
+    @staticmethod
+    def xtc_matmul_graph(i: int, j: int, k: int, dtype: str, name: str = "matmul") -> Any:
+        return build_graph("matmul", [i, j, k], dtype, name=name)
+
+    @staticmethod
+    def xtc_relu_graph(i: int, dtype: str, name: str = "relu") -> Any:
+        return build_graph("relu", [i], dtype, name=name)
+
+    @staticmethod
+    def xtc_conv2d_graph(n: int, h: int, w: int, f: int, r: int, s: int, c: int, SH: int, SW: int, dtype: str,
+                         name: str = "conv2d") -> Any:
+        return build_graph("conv2d", [n, h, w, f, r, s, c, SH, SW], dtype, name=name)
+
+    @staticmethod
+    def get_strategy_name(strategy: str) -> str:
+        return Strategies.resolve_name(strategy)
+
+    @staticmethod
+    def get_operation_dims(operator: str, name: str) -> list[int]:
+        return operation_dims(operator, name)
+
+    @staticmethod
+    def list_operations_dims(operator: str) -> None:
+        from ..artifacts import get_operation, list_operations
+
+        for _, name in list_operations(operator):
+            op = get_operation(operator, name)
+            print(f"{name}: {op['dims']}, {op['params']}")
+
+    @staticmethod
+    def list_operators() -> None:
+        for name in OPERATORS:
+            print(name)
+
+    @staticmethod
+    def list_strategies() -> None:
+        for name in Strategies.names(include_aliases=True):
+            print(name)
+
+    @staticmethod
+    def list_optimizers() -> None:
+        from .optimizers import Optimizers
+
+        for name in Optimizers.names():
+            print(name)
+
     @staticmethod
     def strategy_name(strategy: str) -> str:
         """The registered name of `strategy`, whose arguments follow a colon
