@@ -209,3 +209,23 @@ def test_pad_matmul_unpad_seeded(dtype):
     expect = R.unpad(R.matmul(R.pad(x.astype(np.float64), pads), R.pad(y.astype(np.float64), pads)), pads)
     tol = 1e-12 if dtype == "float64" else 1e-5
     assert np.max(np.abs(out - expect)) <= tol * np.max(np.abs(expect))
+
+
+@pytest.mark.gpu
+def test_unpad_of_a_bf16_output():
+    """A bf16 matmul output (stored as 16-bit words after the cast kernel)
+    cropped by unpad: the crop moves 2-byte elements; validate=True on
+    np_init inputs compares with graph.forward, which rounds the same exact
+    sums to bf16."""
+    from xtc_amd.backends.hip import Backend
+    from xtc_amd.backends.hip.lowering import lower_graph
+
+    a = O.tensor((30, 64), "bfloat16", name="A")
+    b = O.tensor((64, 48), "bfloat16", name="B")
+    with O.graph(name="matmul_bf16_unpad") as gb:
+        O.unpad(O.matmul(a, b, name="M"), padding={-2: (1, 3), -1: (2, 2)}, name="C")
+    plan = lower_graph(gb.graph)
+    assert [ln.kind for ln in plan.launches] == ["matmul", "cast", "unpad"] and plan.launches[-1].attrs["elem"] == 2
+    backend = Backend(gb.graph)
+    module = backend.get_compiler().compile(backend.get_scheduler().schedule())
+    assert module.get_executor(validate=True).execute() == 0
