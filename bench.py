@@ -243,7 +243,7 @@ def _print_peaks() -> int:
 
 def _elementwise(steps: int) -> int:
     """HBM rate of the elementwise kernels, one JSON line each: relu, pad,
-    the bf16 casts (library entry points) and the transpose that stages a
+    unpad, the bf16 casts (library entry points) and the transpose that stages a
     transposed matmul operand (timed inside a trans_a matmul with N = 16, so
     its rate is read from the kernel trace: the line's time includes the
     generic GEMM that consumes the copy).  Bytes are algorithmic: every input
@@ -290,6 +290,16 @@ def _elementwise(steps: int) -> int:
         nbytes = 4 * (int(np.prod(shape)) + out_elems)
         timed(f"pad_kernel {'x'.join(map(str, shape))} pads {[list(p) for p in pads]}", nbytes,
               lambda sh=sh, be=be, af=af: capi.check(L.xtc_hip_pad(xp, yp, nd, sh, be, af, 0.0, None), "pad"))
+    # unpad: the crop after a padded matmul or conv reads and writes each kept element once
+    for shape, crops in (((64, 114, 114, 64), ((0, 0), (1, 1), (1, 1), (0, 0))),
+                         ((8, 56, 56, 68), ((0, 0), (0, 0), (0, 0), (1, 3)))):
+        nd = len(shape)
+        sh = (ctypes.c_int64 * nd)(*shape)
+        be = (ctypes.c_int64 * nd)(*[c[0] for c in crops])
+        af = (ctypes.c_int64 * nd)(*[c[1] for c in crops])
+        kept = int(np.prod([d - c[0] - c[1] for d, c in zip(shape, crops)]))
+        timed(f"unpad_kernel {'x'.join(map(str, shape))} crops {[list(c) for c in crops]}", 8 * kept,
+              lambda sh=sh, be=be, af=af: capi.check(L.xtc_hip_unpad(xp, yp, 4, nd, sh, be, af, None), "unpad"))
     # transposed A: the library stages A^T [K][M] into A [M][K] with transpose_kernel
     for dtype, esz in (("float32", 4), ("bfloat16", 2)):
         d = capi.MatmulDesc(dtype=capi.XTC_HIP_F32 if dtype == "float32" else capi.XTC_HIP_BF16, M=8192, N=16,
