@@ -599,7 +599,7 @@ def test_pipeline_depth_queries():
     assert capi.matmul_pipeline_depths(d) == [4, 3, 5]  # B^T read natively by the ping-pong kernel
     c = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=8, H=56, W=56, C=64, F=64, R=3, S=3, stride_h=1, stride_w=1,
                         pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)
-    assert capi.conv2d_pipeline_depths(c) == [3]  # direct conv 8x14: a register ring of 3 weight taps
+    assert capi.conv2d_pipeline_depths(c) == [3]  # direct conv 7x14: a register ring of 3 weight taps
     d = capi.MatmulDesc(dtype=7, M=1, N=1, K=1)
     with pytest.raises(capi.HipError, match="bad dtype"):
         capi.matmul_pipeline_depths(d)
@@ -620,10 +620,11 @@ def test_conv_pipeline_depths_describe_the_channel_staged_kernel():
         assert capi.conv2d_pipeline_depths(_conv_c(3, tile, sk)) == capi.conv2d_pipeline_depths(_conv_c(4, tile, sk))
     assert capi.conv2d_pipeline_depths(_conv_c(3, (64, 64, 16, 2, 2), 4)) == [4]  # register ring under split-K
     # the direct-only tile needs 64-channel multiples: not runnable at C = 3 or 4
-    for C in (3, 4):
-        with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
-            capi.conv2d_pipeline_depths(_conv_c(C, (112, 64, 16, 1, 4)))
-    assert capi.conv2d_pipeline_depths(_conv_c(64, (112, 64, 16, 1, 4))) == [3]
+    for tile in ((112, 64, 16, 1, 4), (98, 64, 16, 1, 4)):
+        for C in (3, 4):
+            with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
+                capi.conv2d_pipeline_depths(_conv_c(C, tile))
+        assert capi.conv2d_pipeline_depths(_conv_c(64, tile)) == [3]
     # a non-finite pad value cannot be staged (inf * 0 is NaN): the scalar kernel
     assert capi.conv2d_pipeline_depths(_conv_c(3, pad_value=float("inf"))) == [1]
 
@@ -813,15 +814,17 @@ def test_instances_and_default_tile():
 
 
 def test_conv_default_tile_direct_block():
-    # the 8x14 direct conv block replaces the 8x8 one for windows wider than
-    # 1x1 whose 8x14 blocks fit in one wave of 256 CUs
+    # a 1x4-wave direct conv block replaces the 8x8 one for windows wider
+    # than 1x1 whose blocks fit in one wave of 256 CUs: 7x14 where its blocks
+    # do, else 8x14
     def tile(n, h, w, c, f, r, pad):
         d = capi.Conv2dDesc(dtype=capi.XTC_HIP_F32, N=n, H=h, W=w, C=c, F=f, R=r, S=r, stride_h=1, stride_w=1,
                             pad_top=pad, pad_bottom=pad, pad_left=pad, pad_right=pad)
         return capi.conv2d_default_tile(d)[0]
 
-    assert tile(8, 56, 56, 64, 64, 3, 1) == (112, 64, 16, 1, 4)      # C4: 224 blocks
-    assert tile(1, 70, 70, 128, 256, 3, 0) == (112, 64, 16, 1, 4)    # Yolo9000_08: 180 blocks
+    assert tile(8, 56, 56, 64, 64, 3, 1) == (98, 64, 16, 1, 4)       # C4: 256 blocks (224 of 8x14)
+    assert tile(1, 70, 70, 128, 256, 3, 0) == (98, 64, 16, 1, 4)     # Yolo9000_08: 200 blocks
+    assert tile(1, 115, 226, 64, 64, 3, 0) == (112, 64, 16, 1, 4)    # 113x224: 272 of 7x14, 240 of 8x14
     assert tile(1, 138, 138, 64, 128, 3, 0) == (64, 64, 16, 2, 2)    # Yolo9000_04: 340 blocks
     assert tile(1, 68, 68, 256, 128, 1, 0) == (64, 64, 16, 2, 2)     # Yolo9000_09: 1x1
     assert tile(1, 56, 56, 64, 64, 1, 0) == (64, 64, 16, 2, 2)       # ResNet18_03: 1x1

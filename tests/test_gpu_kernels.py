@@ -285,7 +285,7 @@ def test_conv_stride_asym_pad_value(dtype):
 
 def test_every_conv_instance():
     # tiles that exist only in the direct conv kernel (C and F multiples of
-    # 64) have no kernel for this shape; test_direct_conv_8x14_* cover them
+    # 64) have no kernel for this shape; test_direct_conv_wide_* cover them
     failures = []
     for inst in _instances(True):
         dtype = inst["dtype"]
@@ -295,7 +295,7 @@ def test_every_conv_instance():
         try:
             capi.conv2d_pipeline_depths(probe)
         except capi.HipError:
-            assert inst["tile"] == (112, 64, 16, 1, 4), inst
+            assert inst["tile"] in WIDE_DIRECT_TILES, inst
             continue
         x = ref.np_init((2, 10, 12, 16), "float32")
         w = (ref.np_init((3, 3, 16, 32), "float32")[::-1]).copy()
@@ -1037,26 +1037,55 @@ def test_direct_conv_8x14_tile_matches_8x8():
     assert ref.scaled_error(a, ref.relu(ref.conv2d(xsp, ws)), 576, np.abs(xsp).max(), np.abs(ws).max()) <= TOL_F32
 
 
+def test_direct_conv_7x14_tile():
+    # the 7x14-pixel, 1x4-wave tile (98x64x16, 256 blocks for C4): 6 whole
+    # 16-pixel tiles per wave as on the 8x14 tile, and the block's last 2
+    # pixels on 4x4x1 MFMAs.  Exact on integer inputs; on the seeded C4
+    # inputs the whole-tile pixels are bit-identical to the 8x8 tile (same
+    # MFMA order), the 2 remainder pixels of each block sum their channels
+    # in four phases and are within fp32 rounding
+    x = ref.np_init((8, 56, 56, 64), "float32") % 5
+    w = ref.np_init((3, 3, 64, 64), "float32") % 3 - 1
+    xp = ref.pad(x, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    want = ref.relu(ref.conv2d(xp, w)).astype(np.float32)
+    got = run_conv(x, w, pads=(1, 1, 1, 1), tile=(98, 64, 16, 1, 4), relu=True)
+    np.testing.assert_array_equal(got, want)
+    xs, ws = ref.config_inputs("C4")
+    a = run_conv(xs, ws, pads=(1, 1, 1, 1), tile=(98, 64, 16, 1, 4), relu=True)
+    b = run_conv(xs, ws, pads=(1, 1, 1, 1), tile=(64, 64, 16, 2, 2), relu=True)
+    oh, ow = np.meshgrid(np.arange(56), np.arange(56), indexing="ij")
+    rem = (oh % 7) * 14 + ow % 14 >= 96  # pixels 96 and 97 of each 7x14 block
+    assert rem.sum() == 2 * 8 * 4
+    np.testing.assert_array_equal(a[:, ~rem], b[:, ~rem])
+    xsp = ref.pad(xs, [(0, 0), (1, 1), (1, 1), (0, 0)])
+    assert ref.scaled_error(a, ref.relu(ref.conv2d(xsp, ws)), 576, np.abs(xsp).max(), np.abs(ws).max()) <= TOL_F32
+
+
+WIDE_DIRECT_TILES = [(112, 64, 16, 1, 4), (98, 64, 16, 1, 4)]
+
+
+@pytest.mark.parametrize("tile", WIDE_DIRECT_TILES, ids=["8x14", "7x14"])
 @pytest.mark.parametrize("shape", [(2, 23, 30, 128, 64, 3, 3, 0), (1, 9, 15, 64, 128, 1, 1, 1), (3, 16, 40, 64, 64, 3, 3, 2)])
-def test_direct_conv_8x14_ragged(shape):
+def test_direct_conv_wide_ragged(shape, tile):
     # partial blocks in H and W, more than one channel chunk, 1x1 windows, pads of 0-2
     n, h, wd, c, f, r, s, pad = shape
     x = rng_uniform(21, (n, h, wd, c))
     w = rng_uniform(22, (r, s, c, f))
-    got = run_conv(x, w, pads=(pad, pad, pad, pad), pad_value=0.25, tile=(112, 64, 16, 1, 4))
+    got = run_conv(x, w, pads=(pad, pad, pad, pad), pad_value=0.25, tile=tile)
     xp = ref.pad(x, [(0, 0), (pad, pad), (pad, pad), (0, 0)], 0.25)
     assert ref.scaled_error(got, ref.conv2d(xp, w), r * s * c, np.abs(xp).max(), 1.0) <= TOL_F32
     # integer inputs: exact, every weight tap of the register ring and every
     # channel chunk (the halo reload between chunks) included
     xi = ref.np_init((n, h, wd, c), "float32") % 5
     wi = ref.np_init((r, s, c, f), "float32") % 3 - 1
-    got = run_conv(xi, wi, pads=(pad, pad, pad, pad), pad_value=2.0, tile=(112, 64, 16, 1, 4))
+    got = run_conv(xi, wi, pads=(pad, pad, pad, pad), pad_value=2.0, tile=tile)
     xpi = ref.pad(xi, [(0, 0), (pad, pad), (pad, pad), (0, 0)], 2.0)
     np.testing.assert_array_equal(got, ref.conv2d(xpi, wi).astype(np.float32))
 
 
+@pytest.mark.parametrize("tile", WIDE_DIRECT_TILES, ids=["8x14", "7x14"])
 @pytest.mark.parametrize("r,s", [(3, 3), (3, 2), (2, 3)])
-def test_direct_conv_8x14_bias_relu(r, s):
+def test_direct_conv_wide_bias_relu(r, s, tile):
     # 3x3 at stride 1 runs the compile-time-offset kernel, the other windows
     # the general one, on the same tile: bias and relu in the epilogue, two
     # filter blocks, blocks that overhang the image in H and W
@@ -1064,19 +1093,20 @@ def test_direct_conv_8x14_bias_relu(r, s):
     w = rng_uniform(52, (r, s, 64, 128), -0.1, 0.1)
     bias = rng_uniform(53, (128,), -0.3, 0.3)
     pads = (r // 2, r // 2, s // 2, s // 2)
-    got = run_conv(x, w, pads=pads, tile=(112, 64, 16, 1, 4), relu=True, bias=bias)
+    got = run_conv(x, w, pads=pads, tile=tile, relu=True, bias=bias)
     xp = ref.pad(x, [(0, 0), pads[:2], pads[2:], (0, 0)])
     want = ref.relu(ref.conv2d(xp, w) + bias)
     assert ref.scaled_error(got, want, r * s * 64, 1.0, 0.1) <= TOL_F32
     xi = ref.np_init(x.shape, "float32") % 5
     wi = ref.np_init(w.shape, "float32") % 3 - 1
     bi = np.arange(128, dtype=np.float32) % 7 - 3
-    got = run_conv(xi, wi, pads=pads, tile=(112, 64, 16, 1, 4), relu=True, bias=bi)
+    got = run_conv(xi, wi, pads=pads, tile=tile, relu=True, bias=bi)
     xpi = ref.pad(xi, [(0, 0), pads[:2], pads[2:], (0, 0)])
     np.testing.assert_array_equal(got, ref.relu(ref.conv2d(xpi, wi) + bi).astype(np.float32))
 
 
-def test_direct_only_conv_tile_rejects_other_shapes():
+@pytest.mark.parametrize("tile", WIDE_DIRECT_TILES, ids=["8x14", "7x14"])
+def test_direct_only_conv_tile_rejects_other_shapes(tile):
     x, w = rng_uniform(1, (1, 20, 20, 64)), rng_uniform(2, (3, 3, 64, 64))
     with pytest.raises(capi.HipError, match="exists only in the direct conv kernel"):
-        run_conv(x, w, stride=(2, 2), tile=(112, 64, 16, 1, 4))
+        run_conv(x, w, stride=(2, 2), tile=tile)

@@ -9,8 +9,8 @@ and operand layouts (A and/or B stored transposed).  Convs: N 1-3, H and W
 the vector, 1x1 to 5x5 windows, strides 1-3, asymmetric pads with a pad
 value, any compiled conv tile, split-K 1-4.  Inputs are integers (1..9 and
 -4..4), so every fp32 sum is exact and the output must equal the float64
-oracle bit for bit.  The cases are drawn once from fixed seeds (424 of
-them, then a wider draw of 2460 from other seeds); each one is checked on
+oracle bit for bit.  The cases are drawn once from fixed seeds (448 of
+them, then a wider draw of 2620 from other seeds); each one is checked on
 the host (the library's own descriptor checks) before its GPU step.
 """
 
@@ -25,6 +25,10 @@ from xtc_amd.runtimes.hip import capi
 from xtc_amd.runtimes.hip.buffer import DeviceBuffer
 
 pytestmark = pytest.mark.gpu
+
+
+# conv tiles only the direct kernel implements (C and F multiples of 64)
+DIRECT_ONLY = {(112, 64, 16, 1, 4), (98, 64, 16, 1, 4)}
 
 
 def _tiles(dtype: str, conv: bool) -> list[tuple[int, ...]]:
@@ -63,7 +67,7 @@ def _conv_cases(n: int, seed: int) -> list[tuple]:
         pads = tuple(int(p) for p in rng.integers(0, 3, size=4))
         if h + pads[0] + pads[1] < r or w + pads[2] + pads[3] < s:
             continue
-        tiles = [t for t in _tiles(dtype, True) if t != (112, 64, 16, 1, 4)]
+        tiles = [t for t in _tiles(dtype, True) if t not in DIRECT_ONLY]
         tile = tiles[int(rng.integers(len(tiles)))]
         split = int(rng.choice([1, 1, 2, 4]))
         out.append((i, dtype, nb, h, w, c, f, r, s, sh, sw, pads, tile, split))
@@ -120,16 +124,19 @@ def test_random_conv_exact(case):
     np.testing.assert_array_equal(got, want)
 
 
-def _direct_conv_cases(n: int, seed: int) -> list[tuple]:
+def _direct_conv_cases(n: int, seed: int, wide: tuple[int, ...] = (112, 64, 16, 1, 4)) -> list[tuple]:
     """fp32 convs the direct kernel takes (C and F multiples of 64, the block's
-    halo within its LDS buffer): half of them 3x3 at stride 1, which run the
-    compile-time-offset kernel on the 8x14 tile."""
+    halo within its LDS buffer): two in three on the 1x4-wave tile `wide`
+    (8x14 pixels, or 7x14 with its 2 pixels on 4x4x1 MFMAs), the rest on
+    8x8; half of them 3x3 at stride 1, which run the compile-time-offset
+    kernel."""
     rng = np.random.default_rng(seed)
     out = []
-    halo_pix = {(112, 64, 16, 1, 4): (8, 14, 49152 // 272), (64, 64, 16, 2, 2): (8, 8, 32768 // 272)}
+    halo_pix = {(112, 64, 16, 1, 4): (8, 14, 49152 // 272), (98, 64, 16, 1, 4): (7, 14, 49152 // 272),
+                (64, 64, 16, 2, 2): (8, 8, 32768 // 272)}
     while len(out) < n:
         i = len(out)
-        tile = (112, 64, 16, 1, 4) if i % 3 else (64, 64, 16, 2, 2)
+        tile = wide if i % 3 else (64, 64, 16, 2, 2)
         th, tw, cap = halo_pix[tile]
         if i % 2 == 0:
             r = s = 3
@@ -150,10 +157,10 @@ def _direct_conv_cases(n: int, seed: int) -> list[tuple]:
     return out
 
 
-DIRECT = _direct_conv_cases(24, 2026)
+DIRECT = _direct_conv_cases(24, 2026) + _direct_conv_cases(24, 2027, (98, 64, 16, 1, 4))
 
 
-@pytest.mark.parametrize("case", DIRECT, ids=[f"dconv{c[0]}-{c[6]}x{c[7]}s{c[8]}{c[9]}" for c in DIRECT])
+@pytest.mark.parametrize("case", DIRECT, ids=[f"dconv{k}-{c[6]}x{c[7]}s{c[8]}{c[9]}" for k, c in enumerate(DIRECT)])
 def test_random_direct_conv_exact(case):
     i, nb, h, w, c, f, r, s, sh, sw, pads, tile, with_bias = case
     rng = np.random.default_rng(3000 + i)
@@ -169,10 +176,10 @@ def test_random_direct_conv_exact(case):
 
 
 # A wider draw of the same generators from other seeds: 1500 matmuls, 800
-# convs and 160 direct convs more, each exact as above (about 6 s on MI355X).
+# convs and 320 direct convs more, each exact as above (about 6 s on MI355X).
 WIDE_MATMUL = _matmul_cases(1500, 7001)
 WIDE_CONV = _conv_cases(800, 7002)
-WIDE_DIRECT = _direct_conv_cases(160, 7003)
+WIDE_DIRECT = _direct_conv_cases(160, 7003) + _direct_conv_cases(160, 7004, (98, 64, 16, 1, 4))
 
 
 @pytest.mark.parametrize("case", WIDE_MATMUL, ids=[f"wmm{c[0]}-{c[1]}-{c[2]}x{c[3]}x{c[4]}" for c in WIDE_MATMUL])
@@ -185,6 +192,6 @@ def test_wide_random_conv_exact(case):
     test_random_conv_exact(case)
 
 
-@pytest.mark.parametrize("case", WIDE_DIRECT, ids=[f"wdconv{c[0]}" for c in WIDE_DIRECT])
+@pytest.mark.parametrize("case", WIDE_DIRECT, ids=[f"wdconv{k}" for k in range(len(WIDE_DIRECT))])
 def test_wide_random_direct_conv_exact(case):
     test_random_direct_conv_exact(case)

@@ -82,16 +82,43 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n 
 // TH x TW output pixels per workgroup, WM x WN waves, HALO_BYTES of LDS for
 // the input halo of one 64-channel chunk, weights through LDS stages
 // (WRING = 0) or a register ring of WRING taps.
+// The remainder pixels' epilogue (1 x 4-wave blocks whose pixel count is not
+// a multiple of 16): lane (l16, g) register i holds pixel 16 PT + i of the
+// block, filter f, summed over the channels of phase g; the four phases are
+// added across lanes and the lanes of phase 0 store.
+template <int PT, int REM, int TW>
+__device__ __forceinline__ void store_remainder(const DirectConvArgs& a, dconv::f32x4 accr, int img, int oh0,
+                                                int ow0, int f, int g) {
+#pragma unroll
+  for (int i = 0; i < REM; ++i) {
+    accr[i] += __shfl_xor(accr[i], 16);
+    accr[i] += __shfl_xor(accr[i], 32);
+  }
+  if (g != 0) return;
+  const float bf = a.bias ? a.bias[f] : 0.f;
+#pragma unroll
+  for (int i = 0; i < REM; ++i) {
+    const int p = 16 * PT + i;
+    const int oh = oh0 + p / TW, ow = ow0 + p % TW;
+    if (oh >= a.OH || ow >= a.OW) continue;
+    float v = accr[i] + bf;
+    if (a.relu) v = v < a.relu_threshold ? a.relu_threshold : v;
+    a.O[(((size_t)img * a.OH + oh) * a.OW + ow) * a.F + f] = v;
+  }
+}
+
 template <int TH, int TW, int WM, int WN, int HALO_BYTES, int WRING>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_direct_f32(DirectConvArgs a) {
   using namespace dconv;
   constexpr int HALO_MAX_PIX = halo_pix(HALO_BYTES);
-  constexpr int PT = TH * TW / 16 / WM;  // 16-pixel tiles per wave
+  constexpr int PT = TH * TW / 16 / WM;  // whole 16-pixel tiles per wave
+  constexpr int REM = TH * TW - 16 * PT * WM;  // pixels after them (one wave row only)
   constexpr int FT = FB / WN / 16;       // 16-filter tiles per wave
   constexpr bool REG = WRING > 0;
   constexpr int RING = REG ? WRING : STAGES;  // slabs in flight + 1 (LDS) or in registers
   constexpr int WBYTES = REG ? 16 : W_STAGE;
-  static_assert(WM * WN == NW && TH * TW % (16 * WM) == 0 && FB % (16 * WN) == 0, "tiling");
+  static_assert(WM * WN == NW && FB % (16 * WN) == 0, "tiling");
+  static_assert(REM == 0 || (WM == 1 && FT == 1 && REM <= 4), "remainder pixels: 1 x 4 waves, at most 4");
   static_assert(WRING >= 0 && WRING <= 4, "register ring");
   __shared__ __attribute__((aligned(1024))) float halo[HALO_MAX_PIX * CP];
   __shared__ __attribute__((aligned(1024))) unsigned char w0[WBYTES];
@@ -191,11 +218,20 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     pwp[it] = p % TW;
   }
 
+  // remainder pixel of this lane's 4x4x1 rows (see conv_direct_f32_3x3s1)
+  int rph = 0, rpw = 0;
+  if constexpr (REM > 0) {
+    const int p = 16 * PT + min(l16 & 3, REM - 1);
+    rph = p / TW;
+    rpw = p % TW;
+  }
+
   f32x4 acc[PT][FT];
 #pragma unroll
   for (int i = 0; i < PT; ++i)
 #pragma unroll
     for (int j = 0; j < FT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 accr = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if constexpr (REG) {
 #pragma unroll
@@ -230,11 +266,14 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     int aoff[PT];
 #pragma unroll
     for (int it = 0; it < PT; ++it) aoff[it] = ((php[it] * a.sh + r) * HW + pwp[it] * a.sw + sx) * CP + 4 * g;
+    const int roff = ((rph * a.sh + r) * HW + rpw * a.sw + sx) * CP + 4 * g;
 #pragma unroll
     for (int kc = 0; kc < CB / 16; ++kc) {
       f32x4 av[PT];
 #pragma unroll
       for (int it = 0; it < PT; ++it) av[it] = *(const f32x4*)(halo + aoff[it] + kc * 16);
+      f32x4 ar;
+      if constexpr (REM > 0) ar = *(const f32x4*)(halo + roff + kc * 16);
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int c = kc * 16 + 4 * g + st;
@@ -245,6 +284,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
 #pragma unroll
           for (int it = 0; it < PT; ++it)
             acc[it][jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av[it][st], acc[it][jt], 0, 0, 0);
+          if constexpr (REM > 0) accr = __builtin_amdgcn_mfma_f32_4x4x1f32(ar[st], bv, accr, 0, 0, 0);
         }
       }
     }
@@ -276,6 +316,7 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
       *(f32x4*)(out + f) = v;
     }
   }
+  if constexpr (REM > 0) store_remainder<PT, REM, TW>(a, accr, img, oh0, ow0, fb * FB + wn * 16 + l16, g);
 }
 
 // The register-ring path above for a 3x3 window at stride 1, with the window,
@@ -294,15 +335,31 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
 // per-lane base registers, and each weight load adds a constant row offset to
 // a per-lane pointer.  C4: 23.1 -> 20.6 us, bit-identical on integer and
 // random inputs.
+//
+// A block whose pixel count is not a multiple of 16 (TH x TW = 16 PT + REM,
+// REM <= 4) runs its PT whole tiles as above and its last REM pixels on
+// v_mfma_f32_4x4x1_16b_f32, whose 16 independent 4x4 blocks take the same
+// operands the ring and the halo already hold: block b = 4 g + fg of lane
+// (l16, g) multiplies pixel i (rows, i = l16 & 3, clamped to REM - 1) by
+// filters 16 wn + 4 fg .. + 3 (columns) over the channels 16 kc + 4 g + st,
+// so each (tap, k-chunk) adds one ds_read_b128 and 4 of these MFMAs (a quarter
+// of a 16x16x4's cycles) instead of a 16-pixel tile, and the four channel
+// phases g are summed across lanes at the end.  7 x 14 blocks (6 tiles + 2
+// pixels) cover 8x56x56 outputs in 256 blocks, one per CU, with 6.25 tiles
+// of MFMA cycles per SIMD instead of the 7 of 8 x 14 blocks on 224 CUs.  The
+// remainder pixels sum their channels in another order than the tiles, so
+// they are exact on exactly summable inputs and within fp32 rounding
+// otherwise.
 template <int TH, int TW, int WRING>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_direct_f32_3x3s1(DirectConvArgs a) {
   using namespace dconv;
   constexpr int R = 3, S = 3, TAPS = R * S;
   constexpr int HH = TH + R - 1, HW = TW + S - 1;  // halo of one block at stride 1
   constexpr int NPIX = HH * HW;
-  constexpr int PT = TH * TW / 16;  // 16-pixel tiles per wave
+  constexpr int PT = TH * TW / 16;  // whole 16-pixel tiles per wave
+  constexpr int REM = TH * TW - 16 * PT;  // pixels after them, on 4x4x1 MFMAs
   constexpr int RING = WRING;
-  static_assert(TH * TW % 16 == 0, "whole 16-pixel tiles");
+  static_assert(REM <= 4, "at most 4 pixels after the whole tiles");
   static_assert(RING >= 1 && TAPS % RING == 0, "the ring slot of tap t of any chunk is t % RING");
   __shared__ __attribute__((aligned(1024))) float halo[NPIX * CP];
 
@@ -369,9 +426,17 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     abase[it] = ((p / TW) * HW + p % TW) * CP + 4 * g;
   }
 
+  // remainder: the lane's pixel 16 PT + min(l16 & 3, REM - 1) at tap (0, 0), channel 4 g
+  int rbase = 0;
+  if constexpr (REM > 0) {
+    const int p = 16 * PT + min(l16 & 3, REM - 1);
+    rbase = ((p / TW) * HW + p % TW) * CP + 4 * g;
+  }
+
   f32x4 acc[PT];
 #pragma unroll
   for (int i = 0; i < PT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 accr = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < RING; ++t)
     if (t < nslab) load_slab(t, t);
@@ -390,11 +455,14 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
         f32x4 av[PT];
 #pragma unroll
         for (int it = 0; it < PT; ++it) av[it] = *(const f32x4*)(halo + abase[it] + toff + kc * 16);
+        f32x4 ar;
+        if constexpr (REM > 0) ar = *(const f32x4*)(halo + rbase + toff + kc * 16);
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           const float bv = wr[u][kc][st];
 #pragma unroll
           for (int it = 0; it < PT; ++it) acc[it] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av[it][st], acc[it], 0, 0, 0);
+          if constexpr (REM > 0) accr = __builtin_amdgcn_mfma_f32_4x4x1f32(ar[st], bv, accr, 0, 0, 0);
         }
       }
       if (t0 + tap + RING < nslab) load_slab(t0 + tap + RING, u);
@@ -416,6 +484,8 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256))) conv_dire
     }
     *(f32x4*)(a.O + (((size_t)img * a.OH + oh) * a.OW + ow) * F + fb * FB + f) = v;
   }
+
+  if constexpr (REM > 0) store_remainder<PT, REM, TW>(a, accr, img, oh0, ow0, fb * FB + wn * 16 + l16, g);
 }
 
 }  // namespace xtc_hip

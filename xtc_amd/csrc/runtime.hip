@@ -591,9 +591,10 @@ int grid_for(uint64_t n, int block) {
 // waves, and the LDS of the input halo.  8x8 (2x2 waves) shares its tile
 // with a generic implicit-GEMM instance, which runs the shapes the direct
 // kernel does not take; 8x14 (1x4 waves, 224 equal blocks for 8x56x56
-// outputs: one per CU) exists only here.  8x8 streams its weights through
-// LDS stages, 8x14 through a register ring of 3 taps (the faster path for
-// each in one process).
+// outputs) and 7x14 (1x4 waves, 6 whole 16-pixel tiles and 2 pixels on
+// 4x4x1 MFMAs; 256 blocks for 8x56x56, one per CU) exist only here.  8x8
+// streams its weights through LDS stages, the 1x4-wave blocks through a
+// register ring of 3 taps (the faster path for each in one process).
 typedef void (*DirectConvLaunch)(const DirectConvArgs&, dim3, hipStream_t);
 template <int TH, int TW, int WM, int WN, int HALO_BYTES, int WRING>
 void launch_conv_direct(const DirectConvArgs& a, dim3 grid, hipStream_t s) {
@@ -618,6 +619,8 @@ const DirectConvTile kDirectConv[] = {
     {{64, 64, 16, 2, 2}, 8, 8, 32 * 1024, 0, &launch_conv_direct<8, 8, 2, 2, 32 * 1024, 0>, nullptr},
     {{112, 64, 16, 1, 4}, 8, 14, 48 * 1024, 3, &launch_conv_direct<8, 14, 1, 4, 48 * 1024, 3>,
      &launch_conv_direct_3x3s1<8, 14, 3>},
+    {{98, 64, 16, 1, 4}, 7, 14, 48 * 1024, 3, &launch_conv_direct<7, 14, 1, 4, 48 * 1024, 3>,
+     &launch_conv_direct_3x3s1<7, 14, 3>},
 };
 
 bool same_tile(const xtc_hip_tile& a, const xtc_hip_tile& b) {
@@ -1287,20 +1290,29 @@ int launch_direct_conv(const xtc_hip_conv2d_desc& d, const xtc_hip_tile& t, int 
 
 // The tile a conv2d descriptor gets when it leaves `tile` zeroed: the shape
 // class default of default_tile, upgraded from the 8x8 direct conv block to
-// the 8x14 one when the direct kernel takes the shape with it, the window is
-// wider than 1x1 (the 8x14 block shares more of the input halo) and its
-// blocks fit in one wave over the chip's 256 CUs.  Measured on MI355X: C4
-// (8x56x56, 3x3, 224 blocks) 26.8 -> 23.0 us; Yolo9000_08 (68x68, 3x3, 180
-// blocks) 47.6 -> 41.3 us; but Yolo9000_04 (340 blocks) 39.8 -> 41.4 us, and
-// the 1x1 convs lose (Yolo9000_09 10.6 -> 15.6 us, ResNet18_03 5.0 -> 6.8).
+// a 1x4-wave one when the direct kernel takes the shape with it, the window
+// is wider than 1x1 (the wider block shares more of the input halo) and its
+// blocks fit in one wave over the chip's 256 CUs: 7x14 (6.125 tiles of MFMA
+// per wave) where its blocks fit, else 8x14 (7 tiles).  Measured on MI355X:
+// C4 (8x56x56, 3x3) 26.8 us on 8x8, 23.0 on 8x14 (224 blocks), 21.9 -> 20.2
+// us from 8x14 to 7x14 (256 blocks) on the 3x3 stride-1 kernel; Yolo9000_08
+// (68x68, 3x3, 180 blocks) 47.6 -> 41.3 us from 8x8 to 8x14; but
+// Yolo9000_04 (340 blocks) 39.8 -> 41.4 us, and the 1x1 convs lose
+// (Yolo9000_09 10.6 -> 15.6 us, ResNet18_03 5.0 -> 6.8).
 void default_conv_tile(const xtc_hip_conv2d_desc& d, int OH, int OW, xtc_hip_tile* t, int* split_k) {
   default_tile(d.dtype, 1, d.N * OH * OW, d.F, d.R * d.S * d.C, t, split_k);
-  const xtc_hip_tile wide{112, 64, 16, 1, 4};
-  const DirectConvTile* dw = direct_conv_tile(wide);
+  if (d.R * d.S == 1 || !same_tile(*t, xtc_hip_tile{64, 64, 16, 2, 2})) return;
   const void* p = (const void*)(uintptr_t)256;
-  if (!dw || d.R * d.S == 1 || !same_tile(*t, xtc_hip_tile{64, 64, 16, 2, 2})) return;
-  const int64_t blocks = (int64_t)d.N * ((OH + dw->th - 1) / dw->th) * ((OW + dw->tw - 1) / dw->tw) * (d.F / dconv::FB);
-  if (blocks <= 256 && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr)) *t = wide;
+  for (const xtc_hip_tile wide : {xtc_hip_tile{98, 64, 16, 1, 4}, xtc_hip_tile{112, 64, 16, 1, 4}}) {
+    const DirectConvTile* dw = direct_conv_tile(wide);
+    if (!dw) continue;
+    const int64_t blocks =
+        (int64_t)d.N * ((OH + dw->th - 1) / dw->th) * ((OW + dw->tw - 1) / dw->tw) * (d.F / dconv::FB);
+    if (blocks <= 256 && direct_conv_applies(d, wide, *split_k, OH, OW, p, p, p, nullptr)) {
+      *t = wide;
+      return;
+    }
+  }
 }
 
 int launch_lds_dma_gemm(const xtc_hip_matmul_desc& d, const xtc_hip_tile& t, int split_k, int stages, int lda,

@@ -661,7 +661,10 @@ class Strategy_HIP(BaseStrategy):
         depth = in_x[6] if len(in_x) > 6 else None
         if self._conv:
             b, h, w, f, r, s, c = self._dims
-            w1, w2 = min(bm, 8), min(wm, 8)
+            # the block's pixels as h x w tiles: w the largest divisor up to 8
+            # (8 for the power-of-two tiles and 112 = 14 x 8, 7 for 98 = 14 x 7)
+            w1 = max(d for d in range(1, min(bm, 8) + 1) if bm % d == 0)
+            w2 = max(d for d in range(1, min(wm, 8) + 1) if wm % d == 0)
             sch.tile(b, {f"{b}1": 1, f"{b}2": 1})
             sch.tile(h, {f"{h}1": bm // w1, f"{h}2": wm // w2})
             sch.tile(w, {f"{w}1": w1, f"{w}2": w2})
