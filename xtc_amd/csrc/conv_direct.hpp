@@ -10,8 +10,10 @@
 // (GEMM M=25088, N=64, K=576) each tile walks only K=576 and re-reads every
 // input pixel once per filter tap from L2; the global-load latency is then
 // exposed on every slab.  Here a workgroup owns a TH x TW block of output
-// pixels x 64 filters of one image (8x8 with 2x2 waves, or 8x14 with 1x4
-// waves: 224 equal blocks for 8x56x56 outputs, one per CU):
+// pixels x 64 filters of one image (8x8 with 2x2 waves; 8x14 with 1x4
+// waves: 224 equal blocks for 8x56x56 outputs; or 7x14 with 1x4 waves, 256
+// blocks, one on every CU, its last 2 pixels on 4x4x1 MFMAs as described at
+// conv_direct_f32_3x3s1):
 //   * the input halo ((TH-1)*sh+R) x ((TW-1)*sw+S) pixels x 64 channels is
 //     loaded once into LDS (pad_value outside the image), pixel stride 68
 //     floats so the 16 pixels read by a lane group fall on distinct banks;
