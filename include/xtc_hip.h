@@ -262,8 +262,10 @@ int xtc_hip_default_tile(int dtype, int conv, int M, int N, int K, xtc_hip_tile 
 
 /* Tile a conv2d descriptor gets when it leaves `tile` zeroed.  Unlike
  * xtc_hip_default_tile(dtype, 1, ...) it sees the window, strides and pads:
- * the direct conv kernel's wider 8x14-pixel block (tile 112x64x16, 1x4
- * waves) replaces the 8x8 one when its input halo fits. */
+ * for a window wider than 1x1 the direct conv kernel's wider 1x4-wave block
+ * replaces the 8x8 one when its input halo fits and its blocks fit in one
+ * wave of 256 CUs, 7x14 pixels (tile 98x64x16) first, else 8x14 (tile
+ * 112x64x16). */
 int xtc_hip_conv2d_default_tile(const xtc_hip_conv2d_desc *desc, xtc_hip_tile *out, int *split_k);
 
 /* Pipeline depths the kernel that runs `desc` (with 256-byte aligned
